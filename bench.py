@@ -1,0 +1,340 @@
+#!/usr/bin/env python3
+"""Throughput of the HIP tensor-ops kernels on one MI355X.
+
+Step: one pass of the FP16 unary/fused elementwise
+workload -- SiLU and tanh-GELU on [8192, 8192] f16 N(0,1) and SwiGLU
+out = a * silu(b) on [4096, 16384] f16 N(0,1), seed 1 -- with every input
+already resident in HBM. `value` is the step's algorithmic bytes (each input
+read once, each output written once) over the wall time of K steps. Every
+kernel launch is also bracketed by HIP events on the SDK stream (the stream
+the kernels run on) for per-kernel durations; the dominant kernel's
+achieved GB/s against the 8 TB/s HBM peak is `roofline`.
+
+The other BASELINE configs are timed per kernel (events around single
+launches, the 256 MB last-level cache flushed between launches) and reported
+under "kernels". The CPU baseline times the oracle (a single-threaded C
+restatement of the reference's portable path) on a bounded slice of the same
+workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+
+# Algorithmic bytes and elements per call (each distinct input read once +
+# each output written once).
+CFG2 = {
+    "silu_f16": (268_435_456, 67_108_864),
+    "gelu_f16": (268_435_456, 67_108_864),
+    "swiglu_f16": (402_653_184, 67_108_864),
+}
+
+
+class Hip:
+    """HIP runtime calls used for timing (events on the SDK stream)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipMemsetAsync.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t,
+                                            ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+        return e.value
+
+    def record(self, event, stream):
+        assert self.lib.hipEventRecord(event, stream) == 0
+
+    def elapsed_ms(self, start, stop):
+        ms = ctypes.c_float()
+        assert self.lib.hipEventSynchronize(stop) == 0
+        assert self.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop) == 0
+        return ms.value
+
+    def memset(self, ptr, nbytes, stream):
+        assert self.lib.hipMemsetAsync(ptr, 0, nbytes, stream) == 0
+
+
+class Timer:
+    """Pairs of events around launches; durations read after the run."""
+
+    def __init__(self, hip, stream):
+        self.hip, self.stream, self.marks = hip, stream, {}
+        self.pool = []
+
+    def _event(self):
+        return self.pool.pop() if self.pool else self.hip.event()
+
+    def around(self, name, fn):
+        a, b = self._event(), self._event()
+        self.hip.record(a, self.stream)
+        fn()
+        self.hip.record(b, self.stream)
+        self.marks.setdefault(name, []).append((a, b))
+
+    def durations(self):
+        out = {}
+        for name, pairs in self.marks.items():
+            out[name] = [self.hip.elapsed_ms(a, b) for a, b in pairs]
+            for a, b in pairs:
+                self.pool += [a, b]
+        self.marks = {}
+        return out
+
+
+def cfg2_step(sdk, t, timer=None):
+    ops = [("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x_silu"], t["y_silu"])),
+           ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x_gelu"], t["y_gelu"])),
+           ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
+    for name, fn in ops:
+        if timer is None:
+            fn()
+        else:
+            timer.around(name, fn)
+
+
+def cpu_baseline(rows_fraction=4):
+    """Oracle (single thread) on the first 1/rows_fraction of each cfg2 tensor,
+    median of 5 after 1 warmup; reported in the metric's unit (GB/s of the
+    same algorithmic bytes)."""
+    import numpy as np
+    from oracle import Oracle
+    orc = Oracle()
+    x = orc.normal((8192 // rows_fraction, 8192), 1, 0, 0.0, 1.0)
+    a = orc.normal((4096 // rows_fraction, 16384), 1, 1, 0.0, 1.0)
+    b = orc.normal((4096 // rows_fraction, 16384), 1, 2, 0.0, 1.0)
+    times = []
+    for rep in range(6):
+        t0 = time.perf_counter()
+        orc.silu(x)
+        orc.gelu(x)
+        orc.silu_multiply(b, a)
+        dt = time.perf_counter() - t0
+        if rep:
+            times.append(dt)
+    med = statistics.median(times)
+    step_bytes = sum(v[0] for v in CFG2.values()) / rows_fraction
+    del np
+    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle/liboracle.so (C restatement, -O3, 1 thread) on the first 1/"
+                       f"{rows_fraction} of the rows of each cfg2 tensor: SiLU+GELU "
+                       f"[{8192 // rows_fraction},8192], SwiGLU [{4096 // rows_fraction},16384]; "
+                       f"median of 5 after 1 warmup = {med:.3f} s"),
+            "cpu_model": _cpu_model(), "host_cores": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---- per-config kernel suite ------------------------------------------------
+
+def suite(sdk, hip, stream, reps=20):
+    """Each BASELINE config's kernels, events around single launches, the
+    last-level cache flushed (512 MiB memset) before every launch."""
+    flush = sdk.tensor("u8", (512 << 20,))
+    flush_ptr = flush.device_ptr()
+    timer = Timer(hip, stream)
+    results = {}
+
+    def measure(name, fn, alg_bytes, elements, warmup=3):
+        for _ in range(warmup):
+            fn()
+        for _ in range(reps):
+            hip.memset(flush_ptr, 512 << 20, stream)
+            timer.around(name, fn)
+        d = timer.durations()[name]
+        med = statistics.median(d)
+        results[name] = {"median_us": round(med * 1e3, 2), "min_us": round(min(d) * 1e3, 2),
+                         "gbps": round(alg_bytes / (med * 1e-3) / 1e9, 1),
+                         "pct_peak": round(100 * alg_bytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                         "elements_per_s": float(f"{elements / (med * 1e-3):.4g}"),
+                         "bytes": alg_bytes}
+
+    T = sdk.tensor
+    # cfg1: f32 add / mul / row-bias add [1024, 4096]
+    a, b, y = T("f32", (1024, 4096)), T("f32", (1024, 4096)), T("f32", (1024, 4096))
+    bias = T("f32", (4096,))
+    sdk.call("tensor_fill_uniform", a, 0, 0, -1.0, 1.0)
+    sdk.call("tensor_fill_uniform", b, 0, 1, -1.0, 1.0)
+    sdk.call("tensor_fill_uniform", bias, 0, 2, -1.0, 1.0)
+    measure("cfg1_add_f32", lambda: sdk.call("tensor_add_f32", a, b, y), 50_331_648, 4_194_304)
+    measure("cfg1_mul_f32", lambda: sdk.call("tensor_mul_f32", a, b, y), 50_331_648, 4_194_304)
+    measure("cfg1_bias_add_f32", lambda: sdk.call("tensor_bias_add_f32", a, bias, y), 33_570_816, 4_194_304)
+    del a, b, y, bias
+    # cfg2
+    x, yy = T("f16", (8192, 8192)), T("f16", (8192, 8192))
+    sdk.call("tensor_fill_normal", x, 1, 0, 0.0, 1.0)
+    measure("cfg2_silu_f16", lambda: sdk.call("tensor_silu_f16", x, yy), *CFG2["silu_f16"])
+    measure("cfg2_gelu_f16", lambda: sdk.call("tensor_gelu_f16", x, yy), *CFG2["gelu_f16"])
+    del x, yy
+    a, b, o = T("f16", (4096, 16384)), T("f16", (4096, 16384)), T("f16", (4096, 16384))
+    sdk.call("tensor_fill_normal", a, 1, 1, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", b, 1, 2, 0.0, 1.0)
+    measure("cfg2_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", b, a, o), *CFG2["swiglu_f16"])
+    del a, b, o
+    # cfg3
+    x, w, y = T("f16", (16384, 2048)), T("f16", (2048,)), T("f16", (16384, 2048))
+    sdk.call("tensor_fill_normal", x, 3, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_uniform", w, 3, 1, 0.5, 1.5)
+    measure("cfg3_rms_norm_f16", lambda: sdk.call("tensor_rms_norm_f16", x, w, 1e-6, y),
+            134_221_824, 33_554_432)
+    del x, w, y
+    lg, pr = T("f16", (32, 2048, 2048)), T("f16", (32, 2048, 2048))
+    sdk.call("tensor_fill_normal", lg, 3, 2, 0.0, 3.0)
+    measure("cfg3_causal_softmax_f16", lambda: sdk.call("tensor_softmax_f16", lg, 1, pr),
+            536_870_912, 134_217_728)
+    del pr
+    rs = T("f32", (32, 2048))
+    measure("cfg3_row_sum_f16", lambda: sdk.call("tensor_row_sum_f16", lg, rs), 268_697_600, 134_217_728)
+    measure("cfg3_row_max_f16", lambda: sdk.call("tensor_row_max_f16", lg, rs), 268_697_600, 134_217_728)
+    del lg, rs
+    # cfg4: (x.permute(0,2,1,3) + A) * M
+    from inference_c_amd import TensorView
+    B, S, H, D = 16, 1024, 32, 64
+    x, A, M = T("f16", (B, S, H, D)), T("f16", (1, H, 1, D)), T("f16", (B, 1, S, 1))
+    out = T("f16", (B, H, S, D))
+    sdk.call("tensor_fill_normal", x, 4, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_uniform", A, 4, 1, -1.0, 1.0)
+    sdk.call("tensor_fill_uniform", M, 4, 2, -1.0, 1.0)
+    view = TensorView.make((B, H, S, D), (S * H * D, D, H * D, 1), 0)
+    measure("cfg4_permuted_broadcast_f16",
+            lambda: sdk.call("tensor_view_add_mul_f16", x, view, A, M, out), 134_254_592, 33_554_432)
+    del x, A, M, out
+    # cfg5: decoder chain (fused residual+RMSNorm, RoPE q+k, SwiGLU) timed as one chain
+    tok, hid, inter = 4096, 2048, 8192
+    x, r, w = T("f16", (tok, hid)), T("f16", (tok, hid)), T("f16", (hid,))
+    h, n = T("f16", (tok, hid)), T("f16", (tok, hid))
+    q, k = T("f16", (tok, 32, 64)), T("f16", (tok, 32, 64))
+    g, u, o = T("f16", (tok, inter)), T("f16", (tok, inter)), T("f16", (tok, inter))
+    for i, t in enumerate((x, r, q, k, g, u)):
+        sdk.call("tensor_fill_normal", t, 5, i, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", w, 5, 9, 0.0, 1.0)
+
+    def chain():
+        sdk.call("tensor_residual_rms_norm_f16", x, r, w, 1e-6, h, n)
+        sdk.call("tensor_rope_f16", q, k, 32, 32, 64, 10000.0, 0)
+        sdk.call("tensor_silu_multiply_f16", g, u, o)
+    measure("cfg5_decoder_chain_f16", chain, 335_548_416, 142_606_336)
+    measure("cfg5_residual_rms_norm_f16",
+            lambda: sdk.call("tensor_residual_rms_norm_f16", x, r, w, 1e-6, h, n), 67_112_960, 8_388_608)
+    measure("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", q, k, 32, 32, 64, 10000.0, 0),
+            67_108_864, 16_777_216)
+    measure("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", g, u, o),
+            201_326_592, 33_554_432)
+    del x, r, w, h, n, q, k, g, u, o
+    big = T("f32", (1 << 30,))
+    sdk.call("tensor_fill_uniform", big, 0, 0, -1.0, 1.0)
+    s64, m32 = T("f64", (1,)), T("f32", (1,))
+    measure("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", big, s64, m32),
+            4_294_967_296, 1_073_741_824)
+    del big
+    sdk.synchronize()
+    return results
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every GPU box here has one "
+                          "GPU and the path shards without communication (see DESIGN.md); "
+                          "run with --gpus 1"}))
+        sys.exit(2)
+
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    sdk.require_device()
+    hip = Hip()
+    stream = sdk.stream()
+
+    t = {}
+    t["x_silu"], t["y_silu"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
+    t["x_gelu"], t["y_gelu"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
+    t["a"], t["b"], t["o"] = (sdk.tensor("f16", (4096, 16384)) for _ in range(3))
+    # separate (identical) SiLU and GELU inputs: the step touches 896 MiB, so
+    # no input is still in the 256 MB last-level cache when it is read again
+    sdk.call("tensor_fill_normal", t["x_silu"], 1, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["x_gelu"], 1, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["a"], 1, 1, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["b"], 1, 2, 0.0, 1.0)
+    sdk.synchronize()
+
+    for _ in range(args.warmup):
+        cfg2_step(sdk, t)
+    sdk.synchronize()
+    timer = Timer(hip, stream)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        cfg2_step(sdk, t, timer)
+    sdk.synchronize()
+    wall = time.perf_counter() - t0
+    per_kernel = {name: sum(d) / len(d) for name, d in timer.durations().items()}
+
+    step_bytes = sum(v[0] for v in CFG2.values())
+    step_elems = sum(v[1] for v in CFG2.values())
+    ms_per_step = wall / args.steps * 1e3
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    dominant = max(per_kernel, key=per_kernel.get)
+    achieved = CFG2[dominant][0] / (per_kernel[dominant] * 1e-3) / 1e9
+    kernels = {name: {"avg_us": round(ms * 1e3, 2),
+                      "gbps": round(CFG2[name][0] / (ms * 1e-3) / 1e9, 1),
+                      "pct_peak": round(100 * CFG2[name][0] / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                      "elements_per_s": float(f"{CFG2[name][1] / (ms * 1e-3):.4g}")}
+               for name, ms in per_kernel.items()}
+    for v in t.values():
+        v.free()
+
+    line = {
+        "metric": "achieved HBM GB/s and % of MI355X peak per tensor_ops kernel; elements/sec",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[1]: SiLU + tanh-GELU on [8192,8192] f16 N(0,1) "
+                               "and SwiGLU a*silu(b) on [4096,16384] f16 N(0,1), seed 1, inputs "
+                               "resident in HBM", "step_bytes": step_bytes,
+                   "elements_per_step": step_elems},
+        "pct_of_peak": round(100 * value / PEAK_GBPS, 1),
+        "elements_per_s": float(f"{step_elems / (ms_per_step * 1e-3):.4g}"),
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                     "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": None},
+        "kernels": kernels,
+    }
+    if not args.no_suite:
+        line["suite"] = suite(sdk, hip, stream)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

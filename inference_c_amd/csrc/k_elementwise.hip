@@ -1,0 +1,284 @@
+// Elementwise and row-broadcast kernels for gfx950.
+//
+// Design: one grid-stride kernel template per arity. Each lane moves 16 bytes
+// per access (global_load_dwordx4 / global_store_dwordx4), UNROLL independent
+// accesses are in flight per lane per iteration, outputs are written with
+// non-temporal stores (streamed once, never re-read by the kernel). The op is
+// a functor on f32 values; f16 inputs are widened exactly and outputs rounded
+// to nearest even by the hardware conversions.
+//
+// Math per op (reference semantics cited in the public headers):
+//   add / mul             one IEEE op (bit-exact against the CPU reference);
+//   silu (f32)            v / (1 + expf(-v)), IEEE divide;
+//   silu (f16 output)     v * rcp(1 + exp2(-v log2 e));
+//   gelu                  x >= 5 -> x, x <= -5 -> 0, else the reference's
+//                         0.5 x (1 + tanh(u)) evaluated as x / (1 + e^(-2u)),
+//                         the same function without the cancellation of
+//                         1 + tanh(u) for u << 0; u = 0.7978845608 (x + 0.044715 x^3)
+//                         is formed in the reference's operation order.
+#include "kern_common.hpp"
+#include "kernels.hpp"
+
+namespace icsdk {
+namespace {
+
+// ---- op functors ---------------------------------------------------------
+
+__device__ inline float gelu_inner(float v) {
+    return 0.7978845608f * (v + 0.044715f * v * v * v);
+}
+
+template <bool kFast>
+__device__ inline float gelu(float v) {
+    const float u = gelu_inner(v);
+    float r;
+    if constexpr (kFast) {
+        r = v * fast_rcp(1.0f + fast_exp(-2.0f * u));
+    } else {
+        r = v / (1.0f + expf(-2.0f * u));
+    }
+    r = v >= 5.0f ? v : r;
+    return v <= -5.0f ? 0.0f : r;
+}
+
+template <bool kFast>
+__device__ inline float silu(float v) {
+    if constexpr (kFast) return v * fast_rcp(1.0f + fast_exp(-v));
+    else return v / (1.0f + expf(-v));
+}
+
+template <k::Unary kOp, bool kFast> struct UnaryOp {
+    __device__ inline float operator()(float a, float) const {
+        if constexpr (kOp == k::Unary::Silu) return silu<kFast>(a);
+        else if constexpr (kOp == k::Unary::Gelu) return gelu<kFast>(a);
+        else if constexpr (kOp == k::Unary::Relu) return a > 0.0f ? a : 0.0f;
+        else return a;
+    }
+};
+
+template <k::Binary kOp, bool kFast> struct BinaryOp {
+    __device__ inline float operator()(float a, float b) const {
+        if constexpr (kOp == k::Binary::Add) return a + b;
+        else if constexpr (kOp == k::Binary::Mul) return a * b;
+        else if constexpr (kOp == k::Binary::SiluMul) return silu<kFast>(a) * b;
+        else return gelu<kFast>(a) * b;
+    }
+};
+
+// ---- same-shape map ------------------------------------------------------
+
+constexpr int kUnroll = 4;
+
+template <typename S, int kArity, class Op>
+__device__ inline Vec16<S> apply(const Vec16<S> &a, const Vec16<S> &b, Op op) {
+    Vec16<S> out;
+#pragma unroll
+    for (int e = 0; e < Vec16<S>::N; ++e) {
+        const float x = Elem<S>::load(a.v[e]);
+        const float y = kArity == 2 ? Elem<S>::load(b.v[e]) : 0.0f;
+        out.v[e] = Elem<S>::store(op(x, y));
+    }
+    return out;
+}
+
+template <typename S, int kArity, class Op>
+__global__ __launch_bounds__(kBlock) void map_vec_kernel(const S *__restrict__ a,
+                                                         const S *__restrict__ b,
+                                                         S *__restrict__ y, size_t nvec,
+                                                         size_t n, Op op) {
+    constexpr int E = Vec16<S>::N;
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+    for (; i + (kUnroll - 1) * stride < nvec; i += kUnroll * stride) {
+        Vec16<S> va[kUnroll], vb[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) va[u] = load16_stream(a + (i + u * stride) * E);
+        if constexpr (kArity == 2) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) vb[u] = load16_stream(b + (i + u * stride) * E);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+            store16_stream(y + (i + u * stride) * E, apply<S, kArity>(va[u], vb[u], op));
+    }
+    for (; i < nvec; i += stride) {
+        Vec16<S> va = load16_stream(a + i * E), vb{};
+        if constexpr (kArity == 2) vb = load16_stream(b + i * E);
+        store16_stream(y + i * E, apply<S, kArity>(va, vb, op));
+    }
+    // ragged tail (fewer than one vector)
+    if (blockIdx.x == 0 && threadIdx.x < n - nvec * E) {
+        const size_t t = nvec * E + threadIdx.x;
+        const float x = Elem<S>::load(a[t]);
+        const float z = kArity == 2 ? Elem<S>::load(b[t]) : 0.0f;
+        y[t] = Elem<S>::store(op(x, z));
+    }
+}
+
+// Element-at-a-time variant for operands that are not 16-byte aligned.
+template <typename S, int kArity, class Op>
+__global__ __launch_bounds__(kBlock) void map_scalar_kernel(const S *__restrict__ a,
+                                                            const S *__restrict__ b,
+                                                            S *__restrict__ y, size_t n,
+                                                            Op op) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        const float x = Elem<S>::load(a[i]);
+        const float z = kArity == 2 ? Elem<S>::load(b[i]) : 0.0f;
+        y[i] = Elem<S>::store(op(x, z));
+    }
+}
+
+inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+unsigned grid_for(size_t work_items, size_t per_block) {
+    size_t blocks = (work_items + per_block - 1) / per_block;
+    if (blocks < 1) blocks = 1;
+    if (blocks > (size_t{1} << 20)) blocks = size_t{1} << 20;
+    return (unsigned)blocks;
+}
+
+template <typename S, int kArity, class Op>
+hipError_t launch_map(const S *a, const S *b, S *y, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    constexpr int E = Vec16<S>::N;
+    if (aligned16(a) && aligned16(b) && aligned16(y)) {
+        const size_t nvec = n / E;
+        const unsigned grid = grid_for(nvec > 0 ? nvec : 1, (size_t)kBlock * kUnroll);
+        hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op>), dim3(grid), dim3(kBlock), 0, s,
+                           a, b, y, nvec, n, Op{});
+    } else {
+        hipLaunchKernelGGL((map_scalar_kernel<S, kArity, Op>), dim3(grid_for(n, kBlock * 4)),
+                           dim3(kBlock), 0, s, a, b, y, n, Op{});
+    }
+    return hipGetLastError();
+}
+
+template <typename S, bool kFast>
+hipError_t unary_dispatch(k::Unary op, const S *x, S *y, size_t n, hipStream_t s) {
+    switch (op) {
+        case k::Unary::Silu: return launch_map<S, 1, UnaryOp<k::Unary::Silu, kFast>>(x, nullptr, y, n, s);
+        case k::Unary::Gelu: return launch_map<S, 1, UnaryOp<k::Unary::Gelu, kFast>>(x, nullptr, y, n, s);
+        case k::Unary::Relu: return launch_map<S, 1, UnaryOp<k::Unary::Relu, kFast>>(x, nullptr, y, n, s);
+        case k::Unary::Copy: return launch_map<S, 1, UnaryOp<k::Unary::Copy, kFast>>(x, nullptr, y, n, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <typename S, bool kFast>
+hipError_t binary_dispatch(k::Binary op, const S *a, const S *b, S *y, size_t n,
+                           hipStream_t s) {
+    switch (op) {
+        case k::Binary::Add: return launch_map<S, 2, BinaryOp<k::Binary::Add, kFast>>(a, b, y, n, s);
+        case k::Binary::Mul: return launch_map<S, 2, BinaryOp<k::Binary::Mul, kFast>>(a, b, y, n, s);
+        case k::Binary::SiluMul: return launch_map<S, 2, BinaryOp<k::Binary::SiluMul, kFast>>(a, b, y, n, s);
+        case k::Binary::GeluMul: return launch_map<S, 2, BinaryOp<k::Binary::GeluMul, kFast>>(a, b, y, n, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---- row broadcast (bias) ----------------------------------------------
+
+template <typename S, bool kGelu>
+__device__ inline float bias_value(float x, float b) {
+    const float v = x + b;
+    if constexpr (kGelu) return gelu<sizeof(S) == 2>(v);
+    else return v;
+}
+
+// Vector path: width % E == 0 and 16-byte aligned operands, nvec < 2^32.
+// The column of vector i is i mod (width / E), computed with a multiply-high
+// division; the bias vector is re-read from L1/L2 (it is width*sizeof(S) bytes).
+template <typename S, bool kGelu>
+__global__ __launch_bounds__(kBlock) void bias_vec_kernel(const S *__restrict__ x,
+                                                          const S *__restrict__ bias,
+                                                          S *__restrict__ y, uint32_t nvec,
+                                                          FastDiv per_row) {
+    constexpr int E = Vec16<S>::N;
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < nvec; i += stride) {
+        const uint32_t row = fast_div(i, per_row);
+        const uint32_t col = i - row * per_row.divisor;
+        const Vec16<S> vx = load16_stream(x + (size_t)i * E);
+        const Vec16<S> vb = load16(bias + (size_t)col * E);
+        Vec16<S> out;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            out.v[e] = Elem<S>::store(bias_value<S, kGelu>(Elem<S>::load(vx.v[e]),
+                                                           Elem<S>::load(vb.v[e])));
+        store16_stream(y + (size_t)i * E, out);
+    }
+}
+
+template <typename S, bool kGelu>
+__global__ __launch_bounds__(kBlock) void bias_scalar_kernel(const S *__restrict__ x,
+                                                             const S *__restrict__ bias,
+                                                             S *__restrict__ y, size_t n,
+                                                             size_t width) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = Elem<S>::store(bias_value<S, kGelu>(Elem<S>::load(x[i]),
+                                                   Elem<S>::load(bias[i % width])));
+}
+
+template <typename S, bool kGelu>
+hipError_t launch_bias(const S *x, const S *bias, S *y, size_t rows, size_t width,
+                       hipStream_t s) {
+    const size_t n = rows * width;
+    if (n == 0) return hipSuccess;
+    constexpr int E = Vec16<S>::N;
+    const size_t nvec = n / E;
+    if (width % E == 0 && aligned16(x) && aligned16(bias) && aligned16(y) &&
+        nvec < (size_t{1} << 32)) {
+        hipLaunchKernelGGL((bias_vec_kernel<S, kGelu>), dim3(grid_for(nvec, kBlock * 4)),
+                           dim3(kBlock), 0, s, x, bias, y, (uint32_t)nvec,
+                           make_fast_div((uint32_t)(width / E)));
+    } else {
+        hipLaunchKernelGGL((bias_scalar_kernel<S, kGelu>), dim3(grid_for(n, kBlock * 4)),
+                           dim3(kBlock), 0, s, x, bias, y, n, width);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+namespace k {
+
+hipError_t unary_f32(Unary op, const float *x, float *y, size_t n, hipStream_t s) {
+    return unary_dispatch<float, false>(op, x, y, n, s);
+}
+
+hipError_t unary_f16(Unary op, const uint16_t *x, uint16_t *y, size_t n, hipStream_t s) {
+    return unary_dispatch<_Float16, true>(op, reinterpret_cast<const _Float16 *>(x),
+                                          reinterpret_cast<_Float16 *>(y), n, s);
+}
+
+hipError_t binary_f32(Binary op, const float *a, const float *b, float *y, size_t n,
+                      hipStream_t s) {
+    return binary_dispatch<float, false>(op, a, b, y, n, s);
+}
+
+hipError_t binary_f16(Binary op, const uint16_t *a, const uint16_t *b, uint16_t *y,
+                      size_t n, hipStream_t s) {
+    return binary_dispatch<_Float16, true>(op, reinterpret_cast<const _Float16 *>(a),
+                                           reinterpret_cast<const _Float16 *>(b),
+                                           reinterpret_cast<_Float16 *>(y), n, s);
+}
+
+hipError_t bias_add_f32(const float *x, const float *bias, float *y, size_t rows,
+                        size_t width, bool gelu, hipStream_t s) {
+    return gelu ? launch_bias<float, true>(x, bias, y, rows, width, s)
+                : launch_bias<float, false>(x, bias, y, rows, width, s);
+}
+
+hipError_t bias_add_f16(const uint16_t *x, const uint16_t *bias, uint16_t *y,
+                        size_t rows, size_t width, bool gelu, hipStream_t s) {
+    const auto *hx = reinterpret_cast<const _Float16 *>(x);
+    const auto *hb = reinterpret_cast<const _Float16 *>(bias);
+    auto *hy = reinterpret_cast<_Float16 *>(y);
+    return gelu ? launch_bias<_Float16, true>(hx, hb, hy, rows, width, s)
+                : launch_bias<_Float16, false>(hx, hb, hy, rows, width, s);
+}
+
+}  // namespace k
+}  // namespace icsdk

@@ -1,0 +1,666 @@
+// Row reductions over the last dimension for gfx950: RMSNorm (optionally
+// fused with the residual add), LayerNorm, softmax (optionally causal), row
+// sum and row max.
+//
+// Register path: a row is owned by a group of WPR wave64s (WPR = 1 for rows up
+// to 64*8 vectors of 16 bytes, 4 above that). Each lane loads NV 16-byte
+// vectors, interleaved so that every load instruction of the group covers a
+// contiguous span (coalesced), keeps the widened f32 values in registers,
+// reduces them with the DPP wave reduction and, for WPR > 1, combines the
+// per-wave partials through LDS. The row is read from HBM exactly once and
+// the output written once.
+//
+// Streaming path (widths that are not a multiple of the 16-byte vector, or
+// too wide for registers): one 256-thread block per row, scalar accesses,
+// the row re-read for every pass.
+//
+// Accumulation is f32; the order is per-lane sequential then a tree, which
+// differs from the reference's single sequential sum only by rounding.
+#include "kern_common.hpp"
+#include "kernels.hpp"
+
+namespace icsdk {
+namespace {
+
+// ---- group reductions ----------------------------------------------------
+
+template <int WPR>
+__device__ inline float group_sum(float v, float *lds) {
+    v = wave_sum(v);
+    if constexpr (WPR == 1) {
+        return v;
+    } else {
+        const int wave = threadIdx.x / kWave;
+        __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WPR; ++w) total += lds[w];
+        return total;
+    }
+}
+
+template <int WPR>
+__device__ inline float group_max(float v, float *lds) {
+    v = wave_max(v);
+    if constexpr (WPR == 1) {
+        return v;
+    } else {
+        const int wave = threadIdx.x / kWave;
+        __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
+        __syncthreads();
+        float m = lds[0];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) m = fmaxf(m, lds[w]);
+        return m;
+    }
+}
+
+template <int WPR>
+__device__ inline int group_sum_i32(int v, float *lds) {
+    v = wave_sum_i32(v);
+    if constexpr (WPR == 1) {
+        return v;
+    } else {
+        const int wave = threadIdx.x / kWave;
+        __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = __builtin_bit_cast(float, v);
+        __syncthreads();
+        int total = 0;
+#pragma unroll
+        for (int w = 0; w < WPR; ++w) total += __builtin_bit_cast(int, lds[w]);
+        return total;
+    }
+}
+
+// Which row this thread group owns and the thread's index inside the group.
+template <int WPR>
+struct RowSlot {
+    size_t row;
+    uint32_t t;
+    __device__ RowSlot() {
+        if constexpr (WPR == 1) {
+            row = (size_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+            t = threadIdx.x & (kWave - 1);
+        } else {
+            row = blockIdx.x;
+            t = threadIdx.x;
+        }
+    }
+};
+
+template <typename S, int NV, int WPR>
+struct RowRegs {
+    static constexpr int E = Vec16<S>::N;
+    static constexpr uint32_t T = WPR * kWave;
+    float v[NV][E];
+
+    __device__ inline bool valid(int j, uint32_t t, uint32_t vpr) const { return t + j * T < vpr; }
+
+    __device__ inline void load(const S *row, uint32_t t, uint32_t vpr, float fill) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t vi = t + j * T;
+            if (vi < vpr) {
+                const Vec16<S> x = load16_stream(row + (size_t)vi * E);
+#pragma unroll
+                for (int e = 0; e < E; ++e) v[j][e] = Elem<S>::load(x.v[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) v[j][e] = fill;
+            }
+        }
+    }
+};
+
+// ---- RMSNorm / fused residual + RMSNorm ------------------------------------
+
+template <typename S, int NV, int WPR, bool kResidual>
+__global__ __launch_bounds__(kBlock) void rms_norm_kernel(
+    const S *__restrict__ x, const S *__restrict__ residual, S *__restrict__ sum_out,
+    const S *__restrict__ w, S *__restrict__ y, size_t rows, uint32_t width, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    using R = RowRegs<S, NV, WPR>;
+    constexpr int E = R::E;
+    const RowSlot<WPR> slot;
+    if (slot.row >= rows) return;
+    const uint32_t vpr = width / E;
+    const size_t base = slot.row * width;
+    R r;
+    r.load(x + base, slot.t, vpr, 0.0f);
+    if constexpr (kResidual) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t vi = slot.t + j * R::T;
+            if (vi < vpr) {
+                const Vec16<S> rv = load16_stream(residual + base + (size_t)vi * E);
+                Vec16<S> sum;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    sum.v[e] = Elem<S>::store(r.v[j][e] + Elem<S>::load(rv.v[e]));
+                    r.v[j][e] = Elem<S>::load(sum.v[e]);
+                }
+                store16_stream(sum_out + base + (size_t)vi * E, sum);
+            }
+        }
+    }
+    float squares = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < E; ++e) squares += r.v[j][e] * r.v[j][e];
+    squares = group_sum<WPR>(squares, lds);
+    const float scale = 1.0f / sqrtf(squares / (float)width + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t vi = slot.t + j * R::T;
+        if (vi < vpr) {
+            const Vec16<S> wv = load16(w + (size_t)vi * E);
+            Vec16<S> out;
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                out.v[e] = Elem<S>::store(r.v[j][e] * scale * Elem<S>::load(wv.v[e]));
+            store16_stream(y + base + (size_t)vi * E, out);
+        }
+    }
+}
+
+template <typename S, bool kResidual>
+__global__ __launch_bounds__(kBlock) void rms_norm_stream_kernel(
+    const S *__restrict__ x, const S *__restrict__ residual, S *__restrict__ sum_out,
+    const S *__restrict__ w, S *__restrict__ y, size_t rows, size_t width, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    const size_t row = blockIdx.x;
+    if (row >= rows) return;
+    const size_t base = row * width;
+    float squares = 0.0f;
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        float v = Elem<S>::load(x[base + c]);
+        if constexpr (kResidual) {
+            const S s = Elem<S>::store(v + Elem<S>::load(residual[base + c]));
+            sum_out[base + c] = s;
+            v = Elem<S>::load(s);
+        }
+        squares += v * v;
+    }
+    squares = group_sum<kBlock / kWave>(squares, lds);
+    const float scale = 1.0f / sqrtf(squares / (float)width + eps);
+    const S *src = kResidual ? sum_out : x;
+    for (size_t c = threadIdx.x; c < width; c += kBlock)
+        y[base + c] = Elem<S>::store(Elem<S>::load(src[base + c]) * scale * Elem<S>::load(w[c]));
+}
+
+// ---- LayerNorm -----------------------------------------------------------
+
+template <typename S, int NV, int WPR>
+__global__ __launch_bounds__(kBlock) void layer_norm_kernel(
+    const S *__restrict__ x, const S *__restrict__ scale, const S *__restrict__ bias,
+    S *__restrict__ y, size_t rows, uint32_t width, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    using R = RowRegs<S, NV, WPR>;
+    constexpr int E = R::E;
+    const RowSlot<WPR> slot;
+    if (slot.row >= rows) return;
+    const uint32_t vpr = width / E;
+    const size_t base = slot.row * width;
+    R r;
+    r.load(x + base, slot.t, vpr, 0.0f);
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < E; ++e) total += r.v[j][e];
+    const float mean = group_sum<WPR>(total, lds) / (float)width;
+    float variance = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (r.valid(j, slot.t, vpr)) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float d = r.v[j][e] - mean;
+                variance += d * d;
+            }
+        }
+    variance = group_sum<WPR>(variance, lds);
+    const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t vi = slot.t + j * R::T;
+        if (vi < vpr) {
+            Vec16<S> sv{}, bv{};
+            if (scale) sv = load16(scale + (size_t)vi * E);
+            if (bias) bv = load16(bias + (size_t)vi * E);
+            Vec16<S> out;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                float v = (r.v[j][e] - mean) * inverse_std;
+                if (scale) v *= Elem<S>::load(sv.v[e]);
+                if (bias) v += Elem<S>::load(bv.v[e]);
+                out.v[e] = Elem<S>::store(v);
+            }
+            store16_stream(y + base + (size_t)vi * E, out);
+        }
+    }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBlock) void layer_norm_stream_kernel(
+    const S *__restrict__ x, const S *__restrict__ scale, const S *__restrict__ bias,
+    S *__restrict__ y, size_t rows, size_t width, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    const size_t row = blockIdx.x;
+    if (row >= rows) return;
+    const S *src = x + row * width;
+    float total = 0.0f;
+    for (size_t c = threadIdx.x; c < width; c += kBlock) total += Elem<S>::load(src[c]);
+    const float mean = group_sum<kBlock / kWave>(total, lds) / (float)width;
+    float variance = 0.0f;
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        const float d = Elem<S>::load(src[c]) - mean;
+        variance += d * d;
+    }
+    variance = group_sum<kBlock / kWave>(variance, lds);
+    const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        float v = (Elem<S>::load(src[c]) - mean) * inverse_std;
+        if (scale) v *= Elem<S>::load(scale[c]);
+        if (bias) v += Elem<S>::load(bias[c]);
+        y[row * width + c] = Elem<S>::store(v);
+    }
+}
+
+// ---- softmax -------------------------------------------------------------
+
+// exp used for the softmax numerators: the hardware exp2 path for f16
+// outputs, the libm-accurate expf for f32 outputs.
+template <typename S>
+__device__ inline float softmax_exp(float x) {
+    if constexpr (sizeof(S) == 2) return fast_exp(x);
+    else return expf(x);
+}
+
+// Causal masking: key k of query row q is kept when k <= q + offset. A
+// vector whose first key is past the limit is never loaded.
+template <typename S, int NV, int WPR>
+__global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x,
+                                                         S *__restrict__ y, size_t rows,
+                                                         uint32_t width, uint32_t q_len,
+                                                         uint32_t causal_offset) {
+    __shared__ float lds[kBlock / kWave];
+    using R = RowRegs<S, NV, WPR>;
+    constexpr int E = R::E;
+    const RowSlot<WPR> slot;
+    if (slot.row >= rows) return;
+    const uint32_t vpr = width / E;
+    const size_t base = slot.row * width;
+    // keys 0..limit are visible
+    const uint64_t limit = q_len ? (uint64_t)(slot.row % q_len) + causal_offset
+                                 : (uint64_t)width;
+    const float neg_inf = -__builtin_inff();
+    R r;
+    float m = neg_inf;
+    int pos_inf = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t vi = slot.t + j * R::T;
+        const uint64_t first = (uint64_t)vi * E;
+        if (vi < vpr && first <= limit) {
+            const Vec16<S> xv = load16_stream(x + base + first);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                float s = Elem<S>::load(xv.v[e]);
+                s = first + e <= limit ? s : neg_inf;
+                r.v[j][e] = s;
+                m = fmaxf(m, s);
+                pos_inf += s == __builtin_inff();
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) r.v[j][e] = neg_inf;
+        }
+    }
+    m = group_max<WPR>(m, lds);
+    pos_inf = group_sum_i32<WPR>(pos_inf, lds);
+    if (m == neg_inf) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < E; ++e) r.v[j][e] = 0.0f;
+    } else if (pos_inf > 0) {
+        const float share = 1.0f / (float)pos_inf;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < E; ++e) r.v[j][e] = r.v[j][e] == __builtin_inff() ? share : 0.0f;
+    } else {
+        float total = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                r.v[j][e] = softmax_exp<S>(r.v[j][e] - m);
+                total += r.v[j][e];
+            }
+        total = group_sum<WPR>(total, lds);
+        const float inverse = 1.0f / total;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (sizeof(S) == 2) r.v[j][e] = r.v[j][e] * inverse;
+                else r.v[j][e] = r.v[j][e] / total;
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t vi = slot.t + j * R::T;
+        if (vi < vpr) {
+            Vec16<S> out;
+#pragma unroll
+            for (int e = 0; e < E; ++e) out.v[e] = Elem<S>::store(r.v[j][e]);
+            store16_stream(y + base + (size_t)vi * E, out);
+        }
+    }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBlock) void softmax_stream_kernel(const S *__restrict__ x,
+                                                                S *__restrict__ y,
+                                                                size_t rows, size_t width,
+                                                                size_t q_len,
+                                                                size_t causal_offset) {
+    __shared__ float lds[kBlock / kWave];
+    constexpr int W = kBlock / kWave;
+    const size_t row = blockIdx.x;
+    if (row >= rows) return;
+    const size_t limit = q_len ? row % q_len + causal_offset : width;
+    const S *src = x + row * width;
+    S *dst = y + row * width;
+    const float neg_inf = -__builtin_inff();
+    float m = neg_inf;
+    int pos_inf = 0;
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        const float s = c <= limit ? Elem<S>::load(src[c]) : neg_inf;
+        m = fmaxf(m, s);
+        pos_inf += s == __builtin_inff();
+    }
+    m = group_max<W>(m, lds);
+    pos_inf = group_sum_i32<W>(pos_inf, lds);
+    if (m == neg_inf) {
+        for (size_t c = threadIdx.x; c < width; c += kBlock) dst[c] = Elem<S>::store(0.0f);
+        return;
+    }
+    if (pos_inf > 0) {
+        const float share = 1.0f / (float)pos_inf;
+        for (size_t c = threadIdx.x; c < width; c += kBlock) {
+            const float s = c <= limit ? Elem<S>::load(src[c]) : neg_inf;
+            dst[c] = Elem<S>::store(s == __builtin_inff() ? share : 0.0f);
+        }
+        return;
+    }
+    float total = 0.0f;
+    for (size_t c = threadIdx.x; c < width; c += kBlock)
+        if (c <= limit) total += softmax_exp<S>(Elem<S>::load(src[c]) - m);
+    total = group_sum<W>(total, lds);
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        const float e = c <= limit ? softmax_exp<S>(Elem<S>::load(src[c]) - m) : 0.0f;
+        dst[c] = Elem<S>::store(e / total);
+    }
+}
+
+// ---- row sum / row max -----------------------------------------------------
+
+template <typename S, int NV, int WPR, bool kMax>
+__global__ __launch_bounds__(kBlock) void row_reduce_kernel(const S *__restrict__ x,
+                                                            float *__restrict__ y,
+                                                            size_t rows, uint32_t width) {
+    __shared__ float lds[kBlock / kWave];
+    using R = RowRegs<S, NV, WPR>;
+    constexpr int E = R::E;
+    const RowSlot<WPR> slot;
+    if (slot.row >= rows) return;
+    const uint32_t vpr = width / E;
+    R r;
+    r.load(x + slot.row * width, slot.t, vpr, kMax ? -__builtin_inff() : 0.0f);
+    float acc = kMax ? -__builtin_inff() : 0.0f;
+    bool has_nan = false;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            if constexpr (kMax) {
+                acc = fmaxf(acc, r.v[j][e]);
+                has_nan |= r.v[j][e] != r.v[j][e];
+            } else {
+                acc += r.v[j][e];
+            }
+        }
+    float result;
+    if constexpr (kMax) {
+        result = group_max<WPR>(acc, lds);
+        const int nan_count = group_sum_i32<WPR>(has_nan ? 1 : 0, lds);
+        if (nan_count) result = __builtin_nanf("");
+    } else {
+        result = group_sum<WPR>(acc, lds);
+    }
+    if (slot.t == 0) y[slot.row] = result;
+}
+
+template <typename S, bool kMax>
+__global__ __launch_bounds__(kBlock) void row_reduce_stream_kernel(const S *__restrict__ x,
+                                                                   float *__restrict__ y,
+                                                                   size_t rows,
+                                                                   size_t width) {
+    __shared__ float lds[kBlock / kWave];
+    constexpr int W = kBlock / kWave;
+    const size_t row = blockIdx.x;
+    if (row >= rows) return;
+    float acc = kMax ? -__builtin_inff() : 0.0f;
+    int nan_count = 0;
+    for (size_t c = threadIdx.x; c < width; c += kBlock) {
+        const float v = Elem<S>::load(x[row * width + c]);
+        if constexpr (kMax) {
+            acc = fmaxf(acc, v);
+            nan_count += v != v;
+        } else {
+            acc += v;
+        }
+    }
+    float result;
+    if constexpr (kMax) {
+        result = group_max<W>(acc, lds);
+        if (group_sum_i32<W>(nan_count, lds)) result = __builtin_nanf("");
+    } else {
+        result = group_sum<W>(acc, lds);
+    }
+    if (threadIdx.x == 0) y[row] = result;
+}
+
+// ---- launch-shape selection --------------------------------------------------
+
+inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+// Register-path shape for a row of `width` elements of size `elem`: returns
+// false when the row must take the streaming path.
+struct RowShape {
+    int nv;
+    int wpr;
+};
+
+inline bool pick_row_shape(size_t width, size_t elem, bool aligned, RowShape *shape) {
+    const size_t per_vec = 16 / elem;
+    if (!aligned || width == 0 || width % per_vec != 0 || width > 0xffffffffu) return false;
+    const size_t vpr = width / per_vec;
+    for (int wpr : {1, 4}) {
+        const size_t threads = (size_t)wpr * kWave;
+        for (int nv : {1, 2, 4, 8}) {
+            if ((size_t)nv * threads >= vpr) {
+                shape->nv = nv;
+                shape->wpr = wpr;
+                return true;
+            }
+        }
+    }
+    return false;
+}
+
+inline dim3 row_grid(size_t rows, int wpr) {
+    const size_t per_block = wpr == 1 ? kBlock / kWave : 1;
+    return dim3((unsigned)((rows + per_block - 1) / per_block));
+}
+
+// Expands a run-time (nv, wpr) into the template instance.
+#define ICSDK_ROW_DISPATCH(shape, KERNEL_TMPL, ...)                                      \
+    do {                                                                                \
+        switch ((shape).wpr * 100 + (shape).nv) {                                        \
+            case 101: KERNEL_TMPL(1, 1); break;                                         \
+            case 102: KERNEL_TMPL(2, 1); break;                                         \
+            case 104: KERNEL_TMPL(4, 1); break;                                         \
+            case 108: KERNEL_TMPL(8, 1); break;                                         \
+            case 401: KERNEL_TMPL(1, 4); break;                                         \
+            case 402: KERNEL_TMPL(2, 4); break;                                         \
+            case 404: KERNEL_TMPL(4, 4); break;                                         \
+            case 408: KERNEL_TMPL(8, 4); break;                                         \
+            default: return hipErrorInvalidValue;                                       \
+        }                                                                               \
+    } while (0)
+
+template <typename S, bool kResidual>
+hipError_t launch_rms(const S *x, const S *residual, S *sum_out, const S *w, S *y,
+                      size_t rows, size_t width, float eps, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    RowShape shape;
+    const bool aligned = aligned16(x) && aligned16(residual) && aligned16(sum_out) &&
+                         aligned16(w) && aligned16(y);
+    if (pick_row_shape(width, sizeof(S), aligned, &shape)) {
+#define ICSDK_RMS(NV, WPR)                                                                 \
+    hipLaunchKernelGGL((rms_norm_kernel<S, NV, WPR, kResidual>), row_grid(rows, WPR),       \
+                       dim3(kBlock), 0, s, x, residual, sum_out, w, y, rows,              \
+                       (uint32_t)width, eps)
+        ICSDK_ROW_DISPATCH(shape, ICSDK_RMS);
+#undef ICSDK_RMS
+    } else {
+        hipLaunchKernelGGL((rms_norm_stream_kernel<S, kResidual>), dim3((unsigned)rows),
+                           dim3(kBlock), 0, s, x, residual, sum_out, w, y, rows, width, eps);
+    }
+    return hipGetLastError();
+}
+
+template <typename S>
+hipError_t launch_layer(const S *x, const S *scale, const S *bias, S *y, size_t rows,
+                        size_t width, float eps, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    RowShape shape;
+    const bool aligned = aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y);
+    if (pick_row_shape(width, sizeof(S), aligned, &shape)) {
+#define ICSDK_LN(NV, WPR)                                                                  \
+    hipLaunchKernelGGL((layer_norm_kernel<S, NV, WPR>), row_grid(rows, WPR), dim3(kBlock), \
+                       0, s, x, scale, bias, y, rows, (uint32_t)width, eps)
+        ICSDK_ROW_DISPATCH(shape, ICSDK_LN);
+#undef ICSDK_LN
+    } else {
+        hipLaunchKernelGGL((layer_norm_stream_kernel<S>), dim3((unsigned)rows), dim3(kBlock),
+                           0, s, x, scale, bias, y, rows, width, eps);
+    }
+    return hipGetLastError();
+}
+
+template <typename S>
+hipError_t launch_softmax(const S *x, S *y, size_t rows, size_t width, size_t q_len,
+                          hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const size_t offset = q_len && width > q_len ? width - q_len : 0;
+    RowShape shape;
+    const bool aligned = aligned16(x) && aligned16(y);
+    if (q_len <= 0xffffffffu && pick_row_shape(width, sizeof(S), aligned, &shape)) {
+#define ICSDK_SM(NV, WPR)                                                                  \
+    hipLaunchKernelGGL((softmax_kernel<S, NV, WPR>), row_grid(rows, WPR), dim3(kBlock), 0, \
+                       s, x, y, rows, (uint32_t)width, (uint32_t)q_len, (uint32_t)offset)
+        ICSDK_ROW_DISPATCH(shape, ICSDK_SM);
+#undef ICSDK_SM
+    } else {
+        hipLaunchKernelGGL((softmax_stream_kernel<S>), dim3((unsigned)rows), dim3(kBlock), 0,
+                           s, x, y, rows, width, q_len, offset);
+    }
+    return hipGetLastError();
+}
+
+template <typename S, bool kMax>
+hipError_t launch_row_reduce(const S *x, float *y, size_t rows, size_t width,
+                             hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    RowShape shape;
+    if (pick_row_shape(width, sizeof(S), aligned16(x), &shape)) {
+#define ICSDK_RR(NV, WPR)                                                                  \
+    hipLaunchKernelGGL((row_reduce_kernel<S, NV, WPR, kMax>), row_grid(rows, WPR),         \
+                       dim3(kBlock), 0, s, x, y, rows, (uint32_t)width)
+        ICSDK_ROW_DISPATCH(shape, ICSDK_RR);
+#undef ICSDK_RR
+    } else {
+        hipLaunchKernelGGL((row_reduce_stream_kernel<S, kMax>), dim3((unsigned)rows),
+                           dim3(kBlock), 0, s, x, y, rows, width);
+    }
+    return hipGetLastError();
+}
+
+inline const _Float16 *h(const uint16_t *p) { return reinterpret_cast<const _Float16 *>(p); }
+inline _Float16 *h(uint16_t *p) { return reinterpret_cast<_Float16 *>(p); }
+
+}  // namespace
+
+namespace k {
+
+hipError_t rms_norm_f32(const float *x, const float *w, float *y, size_t rows,
+                        size_t width, float eps, hipStream_t s) {
+    return launch_rms<float, false>(x, nullptr, nullptr, w, y, rows, width, eps, s);
+}
+
+hipError_t rms_norm_f16(const uint16_t *x, const uint16_t *residual, uint16_t *sum_out,
+                        const uint16_t *w, uint16_t *y, size_t rows, size_t width,
+                        float eps, hipStream_t s) {
+    if (residual)
+        return launch_rms<_Float16, true>(h(x), h(residual), h(sum_out), h(w), h(y), rows,
+                                          width, eps, s);
+    return launch_rms<_Float16, false>(h(x), nullptr, nullptr, h(w), h(y), rows, width,
+                                       eps, s);
+}
+
+hipError_t layer_norm_f32(const float *x, const float *scale, const float *bias, float *y,
+                          size_t rows, size_t width, float eps, hipStream_t s) {
+    return launch_layer<float>(x, scale, bias, y, rows, width, eps, s);
+}
+
+hipError_t layer_norm_f16(const uint16_t *x, const uint16_t *scale, const uint16_t *bias,
+                          uint16_t *y, size_t rows, size_t width, float eps, hipStream_t s) {
+    return launch_layer<_Float16>(h(x), h(scale), h(bias), h(y), rows, width, eps, s);
+}
+
+hipError_t softmax_f32(const float *x, float *y, size_t rows, size_t width, size_t q_len,
+                       hipStream_t s) {
+    return launch_softmax<float>(x, y, rows, width, q_len, s);
+}
+
+hipError_t softmax_f16(const uint16_t *x, uint16_t *y, size_t rows, size_t width,
+                       size_t q_len, hipStream_t s) {
+    return launch_softmax<_Float16>(h(x), h(y), rows, width, q_len, s);
+}
+
+hipError_t row_sum_f32(const float *x, float *y, size_t rows, size_t width, hipStream_t s) {
+    return launch_row_reduce<float, false>(x, y, rows, width, s);
+}
+hipError_t row_sum_f16(const uint16_t *x, float *y, size_t rows, size_t width,
+                       hipStream_t s) {
+    return launch_row_reduce<_Float16, false>(h(x), y, rows, width, s);
+}
+hipError_t row_max_f32(const float *x, float *y, size_t rows, size_t width, hipStream_t s) {
+    return launch_row_reduce<float, true>(x, y, rows, width, s);
+}
+hipError_t row_max_f16(const uint16_t *x, float *y, size_t rows, size_t width,
+                       hipStream_t s) {
+    return launch_row_reduce<_Float16, true>(h(x), y, rows, width, s);
+}
+
+}  // namespace k
+}  // namespace icsdk

@@ -1,0 +1,174 @@
+// Device-side building blocks shared by the gfx950 kernels.
+//
+// Everything here is written for CDNA4 wave64: 16-byte (dwordx4) vector
+// accesses, DPP row/broadcast patterns for wave reductions, and the hardware
+// transcendental instructions for the f16-output fast paths.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace icsdk {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- element types -------------------------------------------------------
+
+// Storage type -> arithmetic in f32. f16 uses the hardware conversions
+// (v_cvt_f32_f16 exact widening, v_cvt_f16_f32 round-to-nearest-even with
+// subnormals, overflow to infinity).
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr int kPerVec = 4;
+    __device__ static inline float load(float v) { return v; }
+    __device__ static inline float store(float v) { return v; }
+};
+template <> struct Elem<_Float16> {
+    static constexpr int kPerVec = 8;
+    __device__ static inline float load(_Float16 v) { return (float)v; }
+    __device__ static inline _Float16 store(float v) { return (_Float16)v; }
+};
+
+// 16-byte vector of T with lane access.
+template <typename T> struct Vec16 {
+    static constexpr int N = 16 / sizeof(T);
+    T v[N];
+};
+
+template <typename T>
+__device__ inline Vec16<T> load16(const T *p) {
+    u32x4 raw = *reinterpret_cast<const u32x4 *>(p);
+    return __builtin_bit_cast(Vec16<T>, raw);
+}
+
+template <typename T>
+__device__ inline Vec16<T> load16_stream(const T *p) {
+    u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return __builtin_bit_cast(Vec16<T>, raw);
+}
+
+template <typename T>
+__device__ inline void store16(T *p, const Vec16<T> &value) {
+    *reinterpret_cast<u32x4 *>(p) = __builtin_bit_cast(u32x4, value);
+}
+
+template <typename T>
+__device__ inline void store16_stream(T *p, const Vec16<T> &value) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, value),
+                                reinterpret_cast<u32x4 *>(p));
+}
+
+// ---- fast math for f16-output paths ---------------------------------------
+
+// e^x through v_exp_f32 (2^x). The product x*log2(e) is rounded once, so the
+// relative error grows like |x| * 2^-24; for f16 outputs (2^-11 ulp) this is
+// invisible except at rounding ties.
+__device__ inline float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// 1/x through v_rcp_f32 (1 ulp).
+__device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// ---- wave64 reductions (DPP) --------------------------------------------
+
+template <int kCtrl, int kRowMask = 0xf>
+__device__ inline float dpp_f32(float old_value, float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old_value),
+                                           __builtin_bit_cast(int, v), kCtrl,
+                                           kRowMask, 0xf, false));
+}
+
+template <int kCtrl, int kRowMask = 0xf>
+__device__ inline int dpp_i32(int old_value, int v) {
+    return __builtin_amdgcn_update_dpp(old_value, v, kCtrl, kRowMask, 0xf, false);
+}
+
+// DPP controls (GFX9 encoding).
+constexpr int kQuadSwap1 = 0xb1;     // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4e;     // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kRowBcast15 = 0x142;   // lane 15 of row r -> row r+1
+constexpr int kRowBcast31 = 0x143;   // lane 31 -> rows 2 and 3
+
+// Sum over the 64 lanes; every lane receives the total. The first four steps
+// reduce within 16-lane rows (all lanes valid), the broadcasts fold rows into
+// lane 63, which is then read as a scalar.
+__device__ inline float wave_sum(float v) {
+    v += dpp_f32<kQuadSwap1>(0.0f, v);
+    v += dpp_f32<kQuadSwap2>(0.0f, v);
+    v += dpp_f32<kRowHalfMirror>(0.0f, v);
+    v += dpp_f32<kRowMirror>(0.0f, v);
+    v += dpp_f32<kRowBcast15, 0xa>(0.0f, v);
+    v += dpp_f32<kRowBcast31, 0xc>(0.0f, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ inline int wave_sum_i32(int v) {
+    v += dpp_i32<kQuadSwap1>(0, v);
+    v += dpp_i32<kQuadSwap2>(0, v);
+    v += dpp_i32<kRowHalfMirror>(0, v);
+    v += dpp_i32<kRowMirror>(0, v);
+    v += dpp_i32<kRowBcast15, 0xa>(0, v);
+    v += dpp_i32<kRowBcast31, 0xc>(0, v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Max over the 64 lanes (fmaxf semantics: a NaN operand is ignored).
+__device__ inline float wave_max(float v) {
+    const float lowest = -__builtin_inff();
+    v = fmaxf(v, dpp_f32<kQuadSwap1>(lowest, v));
+    v = fmaxf(v, dpp_f32<kQuadSwap2>(lowest, v));
+    v = fmaxf(v, dpp_f32<kRowHalfMirror>(lowest, v));
+    v = fmaxf(v, dpp_f32<kRowMirror>(lowest, v));
+    v = fmaxf(v, dpp_f32<kRowBcast15, 0xa>(lowest, v));
+    v = fmaxf(v, dpp_f32<kRowBcast31, 0xc>(lowest, v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Double-precision sum over the wave (cross-lane moves through ds_swizzle /
+// ds_bpermute via __shfl_xor; used only once per wave at the end of a grid
+// reduction).
+__device__ inline double wave_sum_f64(double v) {
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+__device__ inline bool wave_any(bool flag) {
+    return __builtin_amdgcn_ballot_w64(flag) != 0;
+}
+
+// ---- integer division by a run-time constant -----------------------------
+
+// q = n / d for 32-bit n via a precomputed multiplier (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the
+// round-up variant with a 33-bit multiplier folded as t + n).
+struct FastDiv {
+    uint32_t divisor;
+    uint32_t multiplier;
+    uint32_t shift;
+};
+
+__host__ inline FastDiv make_fast_div(uint32_t d) {
+    FastDiv f{d, 0, 0};
+    uint32_t s = 0;
+    while ((uint64_t{1} << s) < d) s++;
+    f.shift = s;
+    f.multiplier = (uint32_t)(((uint64_t{1} << 32) * ((uint64_t{1} << s) - d)) / d + 1);
+    return f;
+}
+
+__device__ inline uint32_t fast_div(uint32_t n, const FastDiv &f) {
+    const uint32_t t = __umulhi(n, f.multiplier);
+    return (uint32_t)(((uint64_t)t + n) >> f.shift);
+}
+
+}  // namespace icsdk

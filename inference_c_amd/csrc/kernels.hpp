@@ -1,0 +1,104 @@
+// Host-side launch interface of the gfx950 kernels (the library's internal
+// HIP table). Every launcher validates nothing beyond what its kernel needs
+// to stay in bounds; the public entry points validate shapes and dtypes first.
+// All launchers enqueue on `stream` and return the launch status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "safetensors.h"
+
+namespace icsdk {
+namespace k {
+
+enum class Unary { Silu, Gelu, Relu, Copy };
+enum class Binary { Add, Mul, SiluMul, GeluMul };
+
+// y[i] = op(x[i]) / op(a[i], b[i]); T is float or f16 (uint16_t storage).
+hipError_t unary_f32(Unary op, const float *x, float *y, size_t n, hipStream_t s);
+hipError_t unary_f16(Unary op, const uint16_t *x, uint16_t *y, size_t n, hipStream_t s);
+hipError_t binary_f32(Binary op, const float *a, const float *b, float *y, size_t n,
+                      hipStream_t s);
+hipError_t binary_f16(Binary op, const uint16_t *a, const uint16_t *b, uint16_t *y,
+                      size_t n, hipStream_t s);
+
+// y[r, c] = x[r, c] + bias[c] (optionally GELU'd).
+hipError_t bias_add_f32(const float *x, const float *bias, float *y, size_t rows,
+                        size_t width, bool gelu, hipStream_t s);
+hipError_t bias_add_f16(const uint16_t *x, const uint16_t *bias, uint16_t *y,
+                        size_t rows, size_t width, bool gelu, hipStream_t s);
+
+// Row normalisation over the last dimension. For rms_norm_f16 a non-null
+// `residual` makes it the fused residual+RMSNorm: sum = f16(x + residual) is
+// written to `sum_out` and normalised.
+hipError_t rms_norm_f32(const float *x, const float *w, float *y, size_t rows,
+                        size_t width, float eps, hipStream_t s);
+hipError_t rms_norm_f16(const uint16_t *x, const uint16_t *residual, uint16_t *sum_out,
+                        const uint16_t *w, uint16_t *y, size_t rows, size_t width,
+                        float eps, hipStream_t s);
+hipError_t layer_norm_f32(const float *x, const float *scale, const float *bias,
+                          float *y, size_t rows, size_t width, float eps,
+                          hipStream_t s);
+hipError_t layer_norm_f16(const uint16_t *x, const uint16_t *scale,
+                          const uint16_t *bias, uint16_t *y, size_t rows,
+                          size_t width, float eps, hipStream_t s);
+
+// Row softmax; q_len == 0: no mask, else causal with query = row % q_len.
+hipError_t softmax_f32(const float *x, float *y, size_t rows, size_t width,
+                       size_t q_len, hipStream_t s);
+hipError_t softmax_f16(const uint16_t *x, uint16_t *y, size_t rows, size_t width,
+                       size_t q_len, hipStream_t s);
+
+// Row sum / max into f32 outputs.
+hipError_t row_sum_f32(const float *x, float *y, size_t rows, size_t width, hipStream_t s);
+hipError_t row_sum_f16(const uint16_t *x, float *y, size_t rows, size_t width,
+                       hipStream_t s);
+hipError_t row_max_f32(const float *x, float *y, size_t rows, size_t width, hipStream_t s);
+hipError_t row_max_f16(const uint16_t *x, float *y, size_t rows, size_t width,
+                       hipStream_t s);
+
+// Two-pass grid reductions. `partials` is device scratch of at least
+// grid_reduce_scratch_bytes() bytes.
+size_t grid_reduce_scratch_bytes();
+hipError_t sum_max_f32(const float *x, size_t n, double *sum_out, float *max_out,
+                       void *partials, hipStream_t s);
+hipError_t argmax_f32(const float *x, size_t n, uint32_t *index_out, void *partials,
+                      hipStream_t s);
+hipError_t argmax_f16(const uint16_t *x, size_t n, uint32_t *index_out, void *partials,
+                      hipStream_t s);
+
+// In-place split-half RoPE on q [seq, qh, dim] and k [seq, kh, dim].
+hipError_t rope_f32(float *q, float *k, size_t seq, size_t qh, size_t kh, size_t dim,
+                    double theta, size_t offset, hipStream_t s);
+hipError_t rope_f16(uint16_t *q, uint16_t *k, size_t seq, size_t qh, size_t kh,
+                    size_t dim, double theta, size_t offset, hipStream_t s);
+
+// Strided view (x + addend) * mult -> contiguous y. Shapes/strides in
+// elements; addend/mult shapes broadcast (1 or equal), either may be null.
+struct ViewArgs {
+    int rank;
+    uint64_t shape[8];
+    int64_t strides[8];
+    uint64_t offset;
+    uint64_t addend_shape[8];
+    uint64_t mult_shape[8];
+};
+hipError_t view_add_mul_f32(const float *x, const ViewArgs &v, const float *addend,
+                            const float *mult, float *y, hipStream_t s);
+hipError_t view_add_mul_f16(const uint16_t *x, const ViewArgs &v, const uint16_t *addend,
+                            const uint16_t *mult, uint16_t *y, hipStream_t s);
+
+// Synthetic inputs (counter-based splitmix64).
+hipError_t fill_uniform(TensorDType dtype, void *y, size_t n, uint64_t seed,
+                        uint64_t stream, float low, float high, hipStream_t s);
+hipError_t fill_normal(TensorDType dtype, void *y, size_t n, uint64_t seed,
+                       uint64_t stream, float mean, float std_dev, hipStream_t s);
+
+// dtype conversion among F32 / F16 / BF16 with the reference's bit rules.
+hipError_t convert(TensorDType from, const void *x, TensorDType to, void *y, size_t n,
+                   hipStream_t s);
+
+}  // namespace k
+}  // namespace icsdk

@@ -1,0 +1,42 @@
+// Internal host-side services of the HIP tensor-ops library: error text,
+// the per-process SDK device/stream, the device staging pool and the
+// grid-reduction scratch.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <mutex>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace icsdk {
+
+void set_error(char *error, size_t capacity, const char *format, ...)
+    __attribute__((format(printf, 3, 4)));
+
+// Lazily initialises the SDK device (the device current on first use) and
+// its stream, once per process. Returns false with a message when no HIP
+// device is usable.
+bool sdk_ready(char *error, size_t capacity);
+hipStream_t sdk_stream();
+int sdk_device();
+// Makes the SDK device current on the calling thread (host threads other
+// than the initialising one may start on another device).
+void bind_device();
+
+// status == hipSuccess, or a message "<what>: <hip error text>".
+bool hip_ok(hipError_t status, const char *what, char *error, size_t capacity);
+
+// Device staging memory for host-storage operands, reused across calls.
+// Blocks are cached by size class until scratch_clear().
+void *scratch_acquire(size_t bytes);
+void scratch_release(void *ptr, size_t bytes);
+void scratch_clear();
+
+// Partial-result buffer of the two-pass grid reductions. The launches of one
+// reduction must be enqueued under grid_reduce_mutex() so that two host
+// threads never interleave their passes on the shared buffer.
+std::mutex &grid_reduce_mutex();
+void *grid_reduce_partials(char *error, size_t capacity);
+
+}  // namespace icsdk

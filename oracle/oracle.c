@@ -1,0 +1,599 @@
+/* CPU oracle for the tensor-ops hot path — TEST INFRASTRUCTURE ONLY.
+ * See oracle.h for what each function follows and how it is pinned.
+ * Compiled with -std=c11 -ffp-contract=off: every float expression below is
+ * evaluated as written, with no fused multiply-add.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- conversions -------------------------------------------------------- */
+
+static uint32_t bits_of(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, sizeof bits);
+    return bits;
+}
+
+static float float_of(uint32_t bits) {
+    float value;
+    memcpy(&value, &bits, sizeof value);
+    return value;
+}
+
+/* Follows src/common/tensor_f16.c:17-42: exact widening; subnormal halves are
+   m * 2^-24 (exact in f32); NaN payload bits move to the top of the f32
+   fraction unchanged. */
+float orc_f16_to_f32(uint16_t value) {
+    const uint32_t sign = (uint32_t)(value & 0x8000u) << 16;
+    const uint32_t exponent = (value >> 10) & 0x1fu;
+    const uint32_t mantissa = value & 0x3ffu;
+    if (exponent == 0x1fu) return float_of(sign | 0x7f800000u | (mantissa << 13));
+    if (exponent != 0) return float_of(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+    const float magnitude = (float)mantissa * 0x1p-24f;
+    return sign ? -magnitude : magnitude;
+}
+
+/* Follows src/common/tensor_f16.c:48-85: round to nearest even; values at or
+   above 65520 become infinity; results below 2^-14 are rounded on the 2^-24
+   grid (subnormals kept, exact ties to even); NaN keeps its sign and top ten
+   payload bits, with a zero payload forced to 1. */
+uint16_t orc_f32_to_f16(float value) {
+    const uint32_t bits = bits_of(value);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const uint32_t magnitude = bits & 0x7fffffffu;
+    if (magnitude > 0x7f800000u) {
+        const uint16_t payload = (uint16_t)((magnitude >> 13) & 0x3ffu);
+        return (uint16_t)(sign | 0x7c00u | (payload ? payload : 1u));
+    }
+    if (magnitude >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 */
+    if (magnitude >= 0x38800000u) {                                   /* >= 2^-14 */
+        const uint32_t rebased = magnitude - 0x38000000u;              /* exponent - 112 */
+        const uint32_t rounded = rebased + 0x0fffu + ((rebased >> 13) & 1u);
+        return (uint16_t)(sign | (rounded >> 13));
+    }
+    if (magnitude <= 0x33000000u) return sign;                        /* <= 2^-25 */
+    const uint32_t exponent = magnitude >> 23;                         /* 102..112 */
+    const uint32_t significand = (magnitude & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126u - exponent;                            /* 14..24 */
+    uint32_t quotient = significand >> shift;
+    const uint32_t remainder = significand & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (remainder > half || (remainder == half && (quotient & 1u))) quotient++;
+    return (uint16_t)(sign | quotient);
+}
+
+/* src/common/tensor_f16.c:44-46 */
+float orc_bf16_to_f32(uint16_t value) { return float_of((uint32_t)value << 16); }
+
+/* src/common/tensor_buffer.c:44-51: NaN is quietened, otherwise RNE. */
+uint16_t orc_f32_to_bf16(float value) {
+    const uint32_t bits = bits_of(value);
+    if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x0040u);
+    return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+void orc_f32_to_bf16_array(const float *x, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_f32_to_bf16(x[i]);
+}
+
+void orc_f16_to_f32_array(const uint16_t *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_f16_to_f32(x[i]);
+}
+
+void orc_f32_to_f16_array(const float *x, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_f32_to_f16(x[i]);
+}
+
+/* ---- synthetic inputs --------------------------------------------------- */
+
+#define GOLDEN_GAMMA 0x9e3779b97f4a7c15ull
+
+/* splitmix64 output function (Steele, Lea, Flood, "Fast splittable
+   pseudorandom number generators", OOPSLA 2014). */
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+uint64_t orc_rng_bits(uint64_t seed, uint64_t stream, uint64_t index) {
+    const uint64_t key = mix64(seed + GOLDEN_GAMMA * (2u * stream + 1u));
+    return mix64(key + GOLDEN_GAMMA * (index + 1u));
+}
+
+static float uniform_value(uint64_t bits, float low, float high) {
+    const float unit = (float)(bits >> 40) * 0x1p-24f;
+    return low + (high - low) * unit;
+}
+
+static float normal_value(uint64_t bits, float mean, float std_dev) {
+    const uint64_t second = mix64(bits ^ 0xd1b54a32d192ed03ull);
+    const double u1 = (double)((bits >> 11) + 1u) * 0x1p-53;   /* (0, 1] */
+    const double u2 = (double)(second >> 11) * 0x1p-53;         /* [0, 1) */
+    const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    return (float)((double)mean + (double)std_dev * z);
+}
+
+void orc_fill_uniform_f32(float *y, size_t n, uint64_t seed, uint64_t stream,
+                          uint64_t first, float low, float high) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = uniform_value(orc_rng_bits(seed, stream, first + i), low, high);
+}
+
+void orc_fill_uniform_f16(uint16_t *y, size_t n, uint64_t seed, uint64_t stream,
+                          uint64_t first, float low, float high) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = orc_f32_to_f16(uniform_value(orc_rng_bits(seed, stream, first + i), low, high));
+}
+
+void orc_fill_normal_f32(float *y, size_t n, uint64_t seed, uint64_t stream,
+                         uint64_t first, float mean, float std_dev) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = normal_value(orc_rng_bits(seed, stream, first + i), mean, std_dev);
+}
+
+void orc_fill_normal_f16(uint16_t *y, size_t n, uint64_t seed, uint64_t stream,
+                         uint64_t first, float mean, float std_dev) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = orc_f32_to_f16(normal_value(orc_rng_bits(seed, stream, first + i), mean, std_dev));
+}
+
+/* ---- elementwise -------------------------------------------------------- */
+
+/* src/common/tensor_graph.c:453-459 */
+void orc_add_f32(const float *a, const float *b, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = a[i] + b[i];
+}
+
+/* closed form: one IEEE multiply */
+void orc_mul_f32(const float *a, const float *b, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = a[i] * b[i];
+}
+
+/* src/common/tensor_ops.c:614-620 */
+void orc_add_f16(const uint16_t *a, const uint16_t *b, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = orc_f32_to_f16(orc_f16_to_f32(a[i]) + orc_f16_to_f32(b[i]));
+}
+
+/* closed form, same widening/rounding as the f16 add */
+void orc_mul_f16(const uint16_t *a, const uint16_t *b, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = orc_f32_to_f16(orc_f16_to_f32(a[i]) * orc_f16_to_f32(b[i]));
+}
+
+/* src/common/tensor_ops.c:554-557 */
+void orc_silu_f32(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = x[i];
+        y[i] = v / (1.0f + expf(-v));
+    }
+}
+
+/* src/common/tensor_ops.c:568-571 */
+void orc_silu_f16(const uint16_t *x, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = orc_f16_to_f32(x[i]);
+        y[i] = orc_f32_to_f16(v / (1.0f + expf(-v)));
+    }
+}
+
+/* tests/smolvlm/src/app/vision_model.c:242-253; the same expression as
+   tensor_compute_cuda.cu:302-305. Evaluated left to right in float:
+   ((0.5*v) * (1 + tanhf(c1 * (v + ((c2*v)*v)*v)))). */
+float orc_gelu_scalar(float v) {
+    if (v >= 5.0f) return v;
+    if (v <= -5.0f) return 0.0f;
+    return 0.5f * v * (1.0f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
+}
+
+/* The same formula, constants and clamps evaluated in double: the arbiter
+   for the cancellation of 1 + tanh(u) near v = -5. */
+double orc_gelu_scalar_f64(double v) {
+    const double c1 = (double)0.7978845608f, c2 = (double)0.044715f;
+    if (v >= 5.0) return v;
+    if (v <= -5.0) return 0.0;
+    return 0.5 * v * (1.0 + tanh(c1 * (v + c2 * v * v * v)));
+}
+
+void orc_gelu_f32(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_gelu_scalar(x[i]);
+}
+
+/* tensor_compute_cuda.cu:310-319 (x >= 5 keeps the input half, which equals
+   rounding the f32 value back) */
+void orc_gelu_f16(const uint16_t *x, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_f32_to_f16(orc_gelu_scalar(orc_f16_to_f32(x[i])));
+}
+
+void orc_gelu_f64(const double *x, double *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = orc_gelu_scalar_f64(x[i]);
+}
+
+/* tensor_compute_cuda.cu:321-331 */
+void orc_gelu_multiply_f16(const uint16_t *x, const uint16_t *gate, uint16_t *y,
+                           size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = orc_f32_to_f16(orc_gelu_scalar(orc_f16_to_f32(x[i])) * orc_f16_to_f32(gate[i]));
+}
+
+/* tensor_compute_cuda.cu:333-336: fmaxf(v, 0) rounded back; NaN and -0
+   give +0. */
+void orc_relu_f16(const uint16_t *x, uint16_t *y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = orc_f16_to_f32(x[i]);
+        y[i] = orc_f32_to_f16(v > 0.0f ? v : 0.0f);
+    }
+}
+
+/* tests/smolvlm/src/app/text_model.c:880-883 and tensor_compute_cuda.cu:363 */
+void orc_silu_multiply_f32(const float *gate, const float *up, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = gate[i];
+        y[i] = v / (1.0f + expf(-v)) * up[i];
+    }
+}
+
+/* tensor_compute_cuda.cu:366-369 (op 1) */
+void orc_silu_multiply_f16(const uint16_t *gate, const uint16_t *up, uint16_t *y,
+                           size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = orc_f16_to_f32(gate[i]);
+        y[i] = orc_f32_to_f16(v / (1.0f + expf(-v)) * orc_f16_to_f32(up[i]));
+    }
+}
+
+/* tensor_compute_cuda.cu:338-347 (i % width broadcast, optional GELU) */
+void orc_bias_add_f32(const float *x, const float *bias, float *y, size_t rows,
+                      size_t width, int gelu) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < width; c++) {
+            const float v = x[r * width + c] + bias[c];
+            y[r * width + c] = gelu ? orc_gelu_scalar(v) : v;
+        }
+}
+
+/* tensor_compute_cuda.cu:349-359 */
+void orc_bias_add_f16(const uint16_t *x, const uint16_t *bias, uint16_t *y,
+                      size_t rows, size_t width, int gelu) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < width; c++) {
+            const float v = orc_f16_to_f32(x[r * width + c]) + orc_f16_to_f32(bias[c]);
+            y[r * width + c] = orc_f32_to_f16(gelu ? orc_gelu_scalar(v) : v);
+        }
+}
+
+/* ---- row reductions ----------------------------------------------------- */
+
+/* src/common/tensor_ops.c:418-428: sequential float sum of squares,
+   scale = 1/sqrtf(sum/width + eps), y = (x * scale) * w */
+void orc_rms_norm_f32(const float *x, const float *w, float *y, size_t rows,
+                      size_t width, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = x + r * width;
+        float squares = 0.0f;
+        for (size_t c = 0; c < width; c++) squares += row[c] * row[c];
+        const float scale = 1.0f / sqrtf(squares / (float)width + eps);
+        for (size_t c = 0; c < width; c++) y[r * width + c] = row[c] * scale * w[c];
+    }
+}
+
+/* src/common/tensor_ops.c:447-457 */
+void orc_rms_norm_f16(const uint16_t *x, const uint16_t *w, uint16_t *y,
+                      size_t rows, size_t width, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        const uint16_t *row = x + r * width;
+        float squares = 0.0f;
+        for (size_t c = 0; c < width; c++) {
+            const float v = orc_f16_to_f32(row[c]);
+            squares += v * v;
+        }
+        const float scale = 1.0f / sqrtf(squares / (float)width + eps);
+        for (size_t c = 0; c < width; c++)
+            y[r * width + c] = orc_f32_to_f16(orc_f16_to_f32(row[c]) * scale * orc_f16_to_f32(w[c]));
+    }
+}
+
+/* src/common/tensor_ops.c:485-503: mean, then sum of squared deviations,
+   inverse_std = 1/sqrtf(var/width + eps), optional scale then bias */
+void orc_layer_norm_f32(const float *x, const float *scale, const float *bias,
+                        float *y, size_t rows, size_t width, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        const float *row = x + r * width;
+        float mean = 0.0f;
+        for (size_t c = 0; c < width; c++) mean += row[c];
+        mean /= (float)width;
+        float variance = 0.0f;
+        for (size_t c = 0; c < width; c++) {
+            const float d = row[c] - mean;
+            variance += d * d;
+        }
+        const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
+        for (size_t c = 0; c < width; c++) {
+            float v = (row[c] - mean) * inverse_std;
+            if (scale) v *= scale[c];
+            if (bias) v += bias[c];
+            y[r * width + c] = v;
+        }
+    }
+}
+
+/* src/common/tensor_ops.c:525-541 */
+void orc_layer_norm_f16(const uint16_t *x, const uint16_t *scale,
+                        const uint16_t *bias, uint16_t *y, size_t rows,
+                        size_t width, float eps) {
+    for (size_t r = 0; r < rows; r++) {
+        const uint16_t *row = x + r * width;
+        float mean = 0.0f;
+        for (size_t c = 0; c < width; c++) mean += orc_f16_to_f32(row[c]);
+        mean /= (float)width;
+        float variance = 0.0f;
+        for (size_t c = 0; c < width; c++) {
+            const float d = orc_f16_to_f32(row[c]) - mean;
+            variance += d * d;
+        }
+        const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
+        for (size_t c = 0; c < width; c++) {
+            float v = (orc_f16_to_f32(row[c]) - mean) * inverse_std;
+            if (scale) v *= orc_f16_to_f32(scale[c]);
+            if (bias) v += orc_f16_to_f32(bias[c]);
+            y[r * width + c] = orc_f32_to_f16(v);
+        }
+    }
+}
+
+/* residual add (tensor_ops.c:614-620) followed by RMSNorm of the stored sum
+   (tensor_ops.c:447-457), as tests/smolvlm/src/app/text_model.c:735 then :701 */
+void orc_residual_rms_norm_f16(const uint16_t *x, const uint16_t *r,
+                               const uint16_t *w, uint16_t *sum, uint16_t *y,
+                               size_t rows, size_t width, float eps) {
+    orc_add_f16(x, r, sum, rows * width);
+    orc_rms_norm_f16(sum, w, y, rows, width, eps);
+}
+
+/* src/common/attention.c:335-380 applied to one row of scores already in
+   `row` (f32). q_len == 0 means no causal mask. */
+static void softmax_row(float *row, size_t width, size_t q_len, size_t q) {
+    const size_t offset = q_len && width > q_len ? width - q_len : 0;
+    float maximum = -INFINITY;
+    size_t positive_infinities = 0;
+    for (size_t k = 0; k < width; k++) {
+        if (q_len && k > q + offset) row[k] = -INFINITY;
+        if (row[k] == INFINITY) positive_infinities++;
+        if (row[k] > maximum) maximum = row[k];
+    }
+    if (maximum == -INFINITY) {
+        for (size_t k = 0; k < width; k++) row[k] = 0.0f;
+        return;
+    }
+    float denominator = 0.0f;
+    if (positive_infinities == 0) {
+        for (size_t k = 0; k < width; k++) {
+            row[k] = expf(row[k] - maximum);
+            denominator += row[k];
+        }
+    } else {
+        denominator = (float)positive_infinities;
+        for (size_t k = 0; k < width; k++) row[k] = row[k] == INFINITY ? 1.0f : 0.0f;
+    }
+    for (size_t k = 0; k < width; k++) row[k] /= denominator;
+}
+
+void orc_softmax_f32(const float *x, float *y, size_t rows, size_t width,
+                     size_t q_len) {
+    for (size_t r = 0; r < rows; r++) {
+        memcpy(y + r * width, x + r * width, width * sizeof(float));
+        softmax_row(y + r * width, width, q_len, q_len ? r % q_len : 0);
+    }
+}
+
+void orc_softmax_f16(const uint16_t *x, uint16_t *y, size_t rows, size_t width,
+                     size_t q_len) {
+    float *row = malloc(width * sizeof(float));
+    if (row == NULL) return;
+    for (size_t r = 0; r < rows; r++) {
+        for (size_t k = 0; k < width; k++) row[k] = orc_f16_to_f32(x[r * width + k]);
+        softmax_row(row, width, q_len, q_len ? r % q_len : 0);
+        for (size_t k = 0; k < width; k++) y[r * width + k] = orc_f32_to_f16(row[k]);
+    }
+    free(row);
+}
+
+/* closed form: float64 accumulation, plus sum |x| for error bounds */
+void orc_row_sum_f32(const float *x, double *sum, double *abs_sum, size_t rows,
+                     size_t width) {
+    for (size_t r = 0; r < rows; r++) {
+        double s = 0.0, a = 0.0;
+        for (size_t c = 0; c < width; c++) {
+            s += (double)x[r * width + c];
+            a += fabs((double)x[r * width + c]);
+        }
+        sum[r] = s;
+        if (abs_sum) abs_sum[r] = a;
+    }
+}
+
+void orc_row_sum_f16(const uint16_t *x, double *sum, double *abs_sum,
+                     size_t rows, size_t width) {
+    for (size_t r = 0; r < rows; r++) {
+        double s = 0.0, a = 0.0;
+        for (size_t c = 0; c < width; c++) {
+            const double v = (double)orc_f16_to_f32(x[r * width + c]);
+            s += v;
+            a += fabs(v);
+        }
+        sum[r] = s;
+        if (abs_sum) abs_sum[r] = a;
+    }
+}
+
+static float max_with_nan(const float *values, size_t n) {
+    float m = -INFINITY;
+    for (size_t i = 0; i < n; i++) {
+        if (isnan(values[i])) return NAN;
+        if (values[i] > m) m = values[i];
+    }
+    return m;
+}
+
+/* closed form: exact max, NaN if the row holds a NaN */
+void orc_row_max_f32(const float *x, float *y, size_t rows, size_t width) {
+    for (size_t r = 0; r < rows; r++) y[r] = max_with_nan(x + r * width, width);
+}
+
+void orc_row_max_f16(const uint16_t *x, float *y, size_t rows, size_t width) {
+    for (size_t r = 0; r < rows; r++) {
+        float m = -INFINITY;
+        for (size_t c = 0; c < width; c++) {
+            const float v = orc_f16_to_f32(x[r * width + c]);
+            if (isnan(v)) { m = NAN; break; }
+            if (v > m) m = v;
+        }
+        y[r] = m;
+    }
+}
+
+/* ---- whole-tensor reductions ------------------------------------------- */
+
+/* closed form: float64 sum and sum |x|, exact max (NaN propagates) */
+void orc_sum_max_f32(const float *x, size_t n, double *sum, double *abs_sum,
+                     float *max) {
+    double s = 0.0, a = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        s += (double)x[i];
+        a += fabs((double)x[i]);
+    }
+    if (sum) *sum = s;
+    if (abs_sum) *abs_sum = a;
+    if (max) *max = max_with_nan(x, n);
+}
+
+/* tensor_compute_cuda.cu:386-397: linear scan from element 0, strict > */
+uint32_t orc_argmax_f32(const float *x, size_t n) {
+    size_t best = 0;
+    float maximum = x[0];
+    for (size_t i = 1; i < n; i++)
+        if (x[i] > maximum) { maximum = x[i]; best = i; }
+    return (uint32_t)best;
+}
+
+uint32_t orc_argmax_f16(const uint16_t *x, size_t n) {
+    size_t best = 0;
+    float maximum = orc_f16_to_f32(x[0]);
+    for (size_t i = 1; i < n; i++) {
+        const float v = orc_f16_to_f32(x[i]);
+        if (v > maximum) { maximum = v; best = i; }
+    }
+    return (uint32_t)best;
+}
+
+/* ---- rope --------------------------------------------------------------- */
+
+/* tests/smolvlm/src/app/text_model.c:477-496 (f32, in place) with the
+   position offset of tensor_compute_cuda.cu:376-383 */
+void orc_rope_f32(float *q, float *k, size_t seq, size_t qh, size_t kh,
+                  size_t dim, double theta, size_t offset) {
+    const size_t half = dim / 2;
+    for (size_t p = 0; p < seq; p++)
+        for (size_t d = 0; d < half; d++) {
+            const float angle = (float)((double)(offset + p) /
+                                        pow(theta, (2.0 * (double)d) / (double)dim));
+            const float c = cosf(angle), s = sinf(angle);
+            for (size_t h = 0; h < qh; h++) {
+                float *base = q + (p * qh + h) * dim;
+                const float left = base[d], right = base[d + half];
+                base[d] = left * c - right * s;
+                base[d + half] = right * c + left * s;
+            }
+            for (size_t h = 0; h < kh; h++) {
+                float *base = k + (p * kh + h) * dim;
+                const float left = base[d], right = base[d + half];
+                base[d] = left * c - right * s;
+                base[d + half] = right * c + left * s;
+            }
+        }
+}
+
+/* tensor_compute_cuda.cu:371-384 with f16 storage */
+void orc_rope_f16(uint16_t *q, uint16_t *k, size_t seq, size_t qh, size_t kh,
+                  size_t dim, double theta, size_t offset) {
+    const size_t half = dim / 2;
+    for (size_t p = 0; p < seq; p++)
+        for (size_t d = 0; d < half; d++) {
+            const float angle = (float)((double)(offset + p) /
+                                        pow(theta, (2.0 * (double)d) / (double)dim));
+            const float c = cosf(angle), s = sinf(angle);
+            for (size_t pass = 0; pass < 2; pass++) {
+                uint16_t *data = pass ? k : q;
+                const size_t heads = pass ? kh : qh;
+                for (size_t h = 0; h < heads; h++) {
+                    uint16_t *base = data + (p * heads + h) * dim;
+                    const float left = orc_f16_to_f32(base[d]);
+                    const float right = orc_f16_to_f32(base[d + half]);
+                    base[d] = orc_f32_to_f16(left * c - right * s);
+                    base[d + half] = orc_f32_to_f16(right * c + left * s);
+                }
+            }
+        }
+}
+
+/* ---- strided views ------------------------------------------------------ */
+
+static size_t broadcast_offset(const uint64_t *shape, size_t rank,
+                               const uint64_t *index) {
+    size_t offset = 0;
+    for (size_t d = 0; d < rank; d++)
+        offset = offset * (size_t)shape[d] + (shape[d] == 1 ? 0 : (size_t)index[d]);
+    return offset;
+}
+
+/* closed form: y[i] = (x[view(i)] + addend[bcast(i)]) * mult[bcast(i)] in f32,
+   rounded to f16 */
+void orc_view_add_mul_f16(const uint16_t *x, size_t rank, const uint64_t *shape,
+                          const int64_t *strides, uint64_t offset,
+                          const uint16_t *addend, const uint64_t *addend_shape,
+                          const uint16_t *mult, const uint64_t *mult_shape,
+                          uint16_t *y) {
+    size_t total = 1;
+    for (size_t d = 0; d < rank; d++) total *= (size_t)shape[d];
+    uint64_t index[16] = {0};
+    for (size_t i = 0; i < total; i++) {
+        size_t rest = i;
+        int64_t source = (int64_t)offset;
+        for (size_t d = rank; d-- > 0;) {
+            index[d] = rest % shape[d];
+            rest /= shape[d];
+            source += (int64_t)index[d] * strides[d];
+        }
+        float v = orc_f16_to_f32(x[source]);
+        if (addend) v = v + orc_f16_to_f32(addend[broadcast_offset(addend_shape, rank, index)]);
+        if (mult) v = v * orc_f16_to_f32(mult[broadcast_offset(mult_shape, rank, index)]);
+        y[i] = orc_f32_to_f16(v);
+    }
+}
+
+void orc_view_add_mul_f32(const float *x, size_t rank, const uint64_t *shape,
+                          const int64_t *strides, uint64_t offset,
+                          const float *addend, const uint64_t *addend_shape,
+                          const float *mult, const uint64_t *mult_shape,
+                          float *y) {
+    size_t total = 1;
+    for (size_t d = 0; d < rank; d++) total *= (size_t)shape[d];
+    uint64_t index[16] = {0};
+    for (size_t i = 0; i < total; i++) {
+        size_t rest = i;
+        int64_t source = (int64_t)offset;
+        for (size_t d = rank; d-- > 0;) {
+            index[d] = rest % shape[d];
+            rest /= shape[d];
+            source += (int64_t)index[d] * strides[d];
+        }
+        float v = x[source];
+        if (addend) v = v + addend[broadcast_offset(addend_shape, rank, index)];
+        if (mult) v = v * mult[broadcast_offset(mult_shape, rank, index)];
+        y[i] = v;
+    }
+}

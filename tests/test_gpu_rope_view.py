@@ -1,0 +1,128 @@
+"""RoPE and strided-view kernels on the GPU against the CPU oracle.
+
+RoPE: f16 within 1 ulp of the oracle (cosf/sinf of the same float angle may
+differ in the last f32 bit); f32 within 2e-6 of the pair magnitude.
+Strided views: bit-exact (one f32 add and one multiply per element)."""
+import numpy as np
+import pytest
+
+from inference_c_amd import TensorView
+from tests.helpers import assert_bits_equal, assert_f16_ulps
+
+pytestmark = pytest.mark.gpu
+F16 = np.float16
+
+
+@pytest.mark.parametrize("device", [True, False])
+@pytest.mark.parametrize("seq,qh,kh,dim,offset", [
+    (4096, 32, 32, 64, 0), (17, 8, 2, 128, 5), (3, 1, 1, 2, 0), (9, 3, 5, 6, 1000),
+    (5, 2, 2, 256, 123456)])
+def test_rope_f16(sdk, orc, seq, qh, kh, dim, offset, device):
+    q = orc.normal((seq, qh, dim), 50, 0, 0.0, 1.0)
+    k = orc.normal((seq, kh, dim), 50, 1, 0.0, 1.0)
+    tq, tk = sdk.from_numpy(q, device=device), sdk.from_numpy(k, device=device)
+    sdk.call("tensor_rope_f16", tq, tk, qh, kh, dim, 10000.0, offset)
+    wq, wk = orc.rope(q, k, qh, kh, dim, 10000.0, offset)
+    assert_f16_ulps(tq.download(), wq, 1, "rope q")
+    assert_f16_ulps(tk.download(), wk, 1, "rope k")
+
+
+@pytest.mark.parametrize("seq,qh,kh,dim,offset", [(64, 4, 2, 64, 0), (7, 3, 3, 10, 77)])
+def test_rope_f32(sdk, orc, seq, qh, kh, dim, offset):
+    q = orc.normal((seq, qh, dim), 51, 0, 0.0, 1.0, "f32")
+    k = orc.normal((seq, kh, dim), 51, 1, 0.0, 1.0, "f32")
+    tq, tk = sdk.from_numpy(q), sdk.from_numpy(k)
+    sdk.call("tensor_rope_f32", tq, tk, qh, kh, dim, 500000.0, offset)
+    wq, wk = orc.rope(q, k, qh, kh, dim, 500000.0, offset)
+    half = dim // 2
+    for got, want, src in ((tq.download(), wq, q), (tk.download(), wk, k)):
+        mag = np.sqrt(src[..., :half] ** 2 + src[..., half:] ** 2)
+        mag = np.concatenate([mag, mag], axis=-1)
+        assert np.all(np.abs(got - want) <= 2e-6 * mag + 1e-30)
+
+
+def test_rope_known_answer(sdk):
+    # reference tests/test_tensor_compute.c:160-168
+    tq = sdk.from_numpy(np.array([1, 0, 1, 0], np.float32))
+    tk = sdk.from_numpy(np.array([1, 0, 1, 0], np.float32))
+    sdk.call("tensor_rope_f32", tq, tk, 1, 1, 2, 10000.0, 0)
+    for t in (tq, tk):
+        assert np.allclose(t.download(), [1, 0, np.cos(1.0), np.sin(1.0)], atol=2e-4)
+
+
+def test_rope_rejects_bad_shapes(sdk):
+    q = sdk.tensor("f16", (10, 4, 64))
+    k = sdk.tensor("f16", (10, 3, 64))
+    ok, msg = sdk.try_call("tensor_rope_f16", q, k, 4, 2, 64, 10000.0, 0)
+    assert not ok and "RoPE requires" in msg
+    ok, _ = sdk.try_call("tensor_rope_f16", q, q, 4, 4, 63, 10000.0, 0)
+    assert not ok
+
+
+def view_case(sdk, orc, x, shape, strides, offset, addend, mult, dtype="f16", device=True):
+    tx = sdk.from_numpy(x, device=device)
+    ta = None if addend is None else sdk.from_numpy(addend, device=device)
+    tm = None if mult is None else sdk.from_numpy(mult, device=device)
+    ty = sdk.tensor(dtype, shape, device)
+    view = TensorView.make(shape, strides, offset)
+    sdk.call(f"tensor_view_add_mul_{dtype}", tx, view, ta, tm, ty)
+    want = orc.view_add_mul(x, shape, strides, offset, addend, mult)
+    assert_bits_equal(ty.download(), want, f"view {shape} {strides}")
+
+
+@pytest.mark.parametrize("device", [True, False])
+def test_config4_permuted_broadcast(sdk, orc, device):
+    """x [16,1024,32,64] read as (0,2,1,3), + A[1,32,1,64],
+    * M[16,1,1024,1], written contiguous [16,32,1024,64]."""
+    B, S, H, D = 16, 1024, 32, 64
+    x = orc.normal((B, S, H, D), 1, 0, 0.0, 1.0)
+    A = orc.uniform((1, H, 1, D), 1, 1, -1.0, 1.0, "f16")
+    M = orc.uniform((B, 1, S, 1), 1, 2, -1.0, 1.0, "f16")
+    view_case(sdk, orc, x, (B, H, S, D), (S * H * D, D, H * D, 1), 0, A, M, device=device)
+
+
+@pytest.mark.parametrize("case", ["vector", "tile", "scalar", "broadcast_x", "offset", "rank1"])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_view_paths(sdk, orc, case, dtype):
+    dt = "f16" if dtype == "f16" else "f32"
+    if case == "vector":       # last dim contiguous
+        x = orc.normal((3, 40, 5, 16), 52, 0, 0.0, 1.0, dt)
+        shape, strides, off = (3, 5, 40, 16), (3200, 16, 80, 1), 0
+        A = orc.uniform((1, 5, 1, 16), 52, 1, -1, 1, dt)
+        M = orc.uniform((3, 1, 40, 1), 52, 2, -1, 1, dt)
+    elif case == "tile":       # transpose of the last two dims
+        x = orc.normal((2, 3, 70, 130), 53, 0, 0.0, 1.0, dt)
+        shape, strides, off = (2, 3, 130, 70), (3 * 70 * 130, 70 * 130, 1, 130), 0
+        A = orc.uniform((1, 3, 130, 1), 53, 1, -1, 1, dt)
+        M = orc.uniform((2, 1, 1, 70), 53, 2, -1, 1, dt)
+    elif case == "scalar":     # odd strides
+        x = orc.normal((1000,), 54, 0, 0.0, 1.0, dt)
+        shape, strides, off = (7, 9), (101, 3), 5
+        A = orc.uniform((7, 1), 54, 1, -1, 1, dt)
+        M = None
+    elif case == "broadcast_x":  # stride 0 repeats x along a dim
+        x = orc.normal((64,), 55, 0, 0.0, 1.0, dt)
+        shape, strides, off = (5, 64), (0, 1), 0
+        A, M = None, orc.uniform((5, 64), 55, 2, -1, 1, dt)
+    elif case == "offset":     # sliced, vector-aligned
+        x = orc.normal((10, 48), 56, 0, 0.0, 1.0, dt)
+        shape, strides, off = (4, 32), (96, 1), 8 if dt == "f16" else 4
+        A, M = orc.uniform((1, 32), 56, 1, -1, 1, dt), orc.uniform((4, 32), 56, 2, -1, 1, dt)
+    else:
+        x = orc.normal((100,), 57, 0, 0.0, 1.0, dt)
+        shape, strides, off = (33,), (3,), 1
+        A, M = orc.uniform((33,), 57, 1, -1, 1, dt), orc.uniform((1,), 57, 2, -1, 1, dt)
+    view_case(sdk, orc, x, shape, strides, off, A, M, dt)
+    view_case(sdk, orc, x, shape, strides, off, None, None, dt)
+
+
+def test_view_rejects_out_of_bounds(sdk):
+    x = sdk.tensor("f16", (100,))
+    y = sdk.tensor("f16", (10, 10))
+    ok, msg = sdk.try_call("tensor_view_add_mul_f16", x, TensorView.make((10, 10), (10, 1), 1), None, None, y)
+    assert not ok and "lies inside the input" in msg
+    ok, msg = sdk.try_call("tensor_view_add_mul_f16", x, TensorView.make((10, 10), (-10, 1), 99), None, None, y)
+    assert not ok
+    bad = sdk.tensor("f16", (3, 10))
+    ok, msg = sdk.try_call("tensor_view_add_mul_f16", x, TensorView.make((10, 10), (10, 1), 0), bad, None, y)
+    assert not ok and "1 or equal" in msg

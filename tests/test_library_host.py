@@ -1,0 +1,169 @@
+"""The HIP library on any machine: it loads, exports every function that
+include/*.h declares, keeps the reference's struct layouts and enum values,
+and its host logic (TensorBuffer bookkeeping, validation messages, backend
+selection) behaves like the reference's. No compute call is made here."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from tests.conftest import REPO
+
+REF_INCLUDE = "/root/reference/include"
+
+
+def test_every_declared_function_is_exported(lib):
+    from inference_c_amd import declared_functions
+    names = declared_functions()
+    assert len(names) >= 70
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def _layout(include_dir, tmp_path, tag):
+    exe = tmp_path / f"abi_{tag}"
+    subprocess.run(["gcc", "-std=c11", "-I", include_dir, "-o", str(exe),
+                    os.path.join(REPO, "oracle", "abi_layout.c")], check=True)
+    return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+
+
+def test_struct_layout_matches_reference_header(tmp_path):
+    if not os.path.isdir(REF_INCLUDE):
+        pytest.skip("reference headers absent")
+    mine = _layout(os.path.join(REPO, "include"), tmp_path, "mine")
+    theirs = _layout(REF_INCLUDE, tmp_path, "ref")
+    assert mine == theirs
+    assert "sizeof TensorComputeBackend 392" in mine
+
+
+def test_dtype_helpers(lib):
+    sizes = {"UNKNOWN": 0, "BOOL": 1, "U8": 1, "I16": 2, "F16": 2, "BF16": 2, "F32": 4,
+             "U32": 4, "F64": 8, "U64": 8}
+    for code in range(16):
+        name = lib.tensor_dtype_name(code).decode()
+        if name in sizes:
+            assert lib.tensor_dtype_size(code) == sizes[name]
+    assert lib.tensor_dtype_name(99).decode() == "UNKNOWN"
+    assert lib.tensor_dtype_size(12) == 2 and lib.tensor_dtype_name(12) == b"F16"
+
+
+def test_host_tensor_buffer_contract(lib):
+    from inference_c_amd import Sdk, SdkError
+    sdk = Sdk()
+    t = sdk.tensor("f32", (2, 5), device=False)
+    assert lib.tensor_buffer_rank(t.handle) == 2
+    assert lib.tensor_buffer_element_count(t.handle) == 10
+    assert lib.tensor_buffer_byte_length(t.handle) == 40
+    assert lib.tensor_buffer_storage(t.handle) == 0
+    assert lib.tensor_buffer_data(t.handle) and lib.tensor_buffer_device_handle_internal(t.handle) is None
+    shape = ctypes.cast(lib.tensor_buffer_shape(t.handle), ctypes.POINTER(ctypes.c_uint64))
+    assert [shape[0], shape[1]] == [2, 5]
+    a = np.arange(10, dtype=np.float32).reshape(2, 5)
+    assert np.array_equal(t.upload(a).download(), a)
+    assert np.all(np.frombuffer(ctypes.string_at(lib.tensor_buffer_data(sdk.tensor("u8", (7,), False).handle), 7), np.uint8) == 0)
+    err = ctypes.create_string_buffer(256)
+    buf = np.zeros(4, np.float32)
+    assert not lib.tensor_buffer_upload(t.handle, 36, buf.ctypes.data, 8, err, 256)
+    assert err.value == b"invalid tensor upload range or pointer"
+    assert not lib.tensor_buffer_download(t.handle, 41, buf.ctypes.data, 0, err, 256)
+    assert err.value == b"invalid tensor download range or pointer"
+    empty = sdk.tensor("f16", (0, 3), device=False)
+    assert lib.tensor_buffer_byte_length(empty.handle) == 0
+    with pytest.raises(SdkError, match="invalid tensor buffer dtype, rank, or shape"):
+        sdk.tensor("f32", (1,) * 17, device=False)
+    with pytest.raises(SdkError, match="exceeds addressable size"):
+        sdk.tensor("f32", (1 << 40, 1 << 40), device=False)
+
+
+def test_out_of_scope_entry_points_fail_with_a_message(lib):
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    a = sdk.tensor("f32", (2, 2), device=False)
+    for name in ("tensor_matmul_f32", "tensor_embedding_lookup_f16"):
+        ok, msg = sdk.try_call(name, a, a, a)
+        assert not ok and "not provided by the HIP tensor-ops library" in msg
+    err = ctypes.create_string_buffer(256)
+    res = ctypes.c_void_p(1)
+    assert not lib.tensor_buffer_load(None, b"w", ctypes.byref(res), err, 256)
+    assert res.value is None and b"tensor stores are not part of" in err.value
+
+
+def test_validation_precedes_device_use(lib):
+    """The reference's messages (src/common/tensor_ops.c) for bad operands,
+    produced before any device is touched."""
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    x16 = sdk.tensor("f16", (2, 4), device=False)
+    w16 = sdk.tensor("f16", (4,), device=False)
+    w3 = sdk.tensor("f16", (3,), device=False)
+    x32 = sdk.tensor("f32", (2, 4), device=False)
+    y16 = sdk.tensor("f16", (2, 4), device=False)
+    cases = [
+        (("tensor_rms_norm_f16", x16, w16, float("nan"), y16),
+         "RMSNorm requires compatible F16 tensors and nonnegative epsilon"),
+        (("tensor_rms_norm_f16", x16, w16, -1.0, y16),
+         "RMSNorm requires compatible F16 tensors and nonnegative epsilon"),
+        (("tensor_rms_norm_f16", x16, w3, 0.0, y16), "RMSNorm weight width does not match input"),
+        (("tensor_rms_norm_f32", x16, w16, 0.0, y16),
+         "RMSNorm requires compatible F32 tensors and nonnegative epsilon"),
+        (("tensor_layer_norm_f16", x16, w3, None, 1e-5, y16),
+         "LayerNorm affine parameter width does not match input"),
+        (("tensor_silu_f16", x32, y16), "SiLU requires same-shaped F16 tensors"),
+        (("tensor_silu_f32", x16, y16), "SiLU requires same-shaped F32 tensors"),
+        (("tensor_residual_add_f16", x16, x32, y16), "F16 residual add requires same-shaped F16 tensors"),
+        (("tensor_residual_add_f16", x16, w16, y16), "F16 residual add requires same-shaped F16 tensors"),
+    ]
+    for args, message in cases:
+        ok, msg = sdk.try_call(*args)
+        assert not ok and msg == message, (args[0], msg)
+
+
+def test_empty_tensors_succeed_without_work(lib):
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    e = sdk.tensor("f16", (0, 8), device=False)
+    w = sdk.tensor("f16", (8,), device=False)
+    assert sdk.try_call("tensor_silu_f16", e, e)[0] == 1
+    assert sdk.try_call("tensor_residual_add_f16", e, e, e)[0] == 1
+    assert sdk.try_call("tensor_rms_norm_f16", e, w, 1e-6, e)[0] == 1
+
+
+def test_backend_selection_without_device(lib, monkeypatch):
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    if sdk.available:
+        pytest.skip("a HIP device is present; covered by the gpu tests")
+    for value in (None, "", "auto", "hip", "cuda", "metal", "qnn", "bogus"):
+        if value is None:
+            monkeypatch.delenv("TENSOR_BACKEND", raising=False)
+        else:
+            monkeypatch.setenv("TENSOR_BACKEND", value)
+        assert lib.tensor_compute_preferred_backend() is None
+    name = ctypes.cast(lib.tensor_compute_hip_backend(), ctypes.POINTER(ctypes.c_char_p))[0]
+    assert name == b"hip"
+    for getter, label in (("tensor_compute_cuda_backend", b"cuda"), ("tensor_compute_metal_backend", b"metal")):
+        table = ctypes.cast(getattr(lib, getter)(), ctypes.POINTER(ctypes.c_void_p))
+        assert ctypes.cast(table[0], ctypes.c_char_p).value == label
+        assert ctypes.CFUNCTYPE(ctypes.c_int)(table[1])() == 0
+
+
+def test_compute_without_device_fails_loudly(lib):
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    if sdk.available:
+        pytest.skip("a HIP device is present")
+    x = sdk.tensor("f16", (4,), device=False).upload(np.ones(4, np.float16))
+    y = sdk.tensor("f16", (4,), device=False)
+    ok, msg = sdk.try_call("tensor_silu_f16", x, y)
+    assert not ok and msg.startswith("HIP device unavailable")
+    ok, msg = sdk.try_call("tensor_residual_add_f16", x, x, y)
+    assert not ok and msg.startswith("HIP device unavailable")
+    err = ctypes.create_string_buffer(256)
+    p = ctypes.c_void_p()
+    assert not lib.tensor_device_buffer_create(16, ctypes.byref(p), err, 256)
+    assert err.value.startswith(b"HIP device unavailable")
+    assert not lib.tensor_device_buffer_create(0, ctypes.byref(p), err, 256)
+    assert err.value == b"device buffer size must be nonzero"
+    assert lib.tensor_device_hip_stream() is None

@@ -1,0 +1,70 @@
+"""The oracle restatement against the reference's own portable C path
+(oracle/_ref/libref.so, compiled from the reference sources), bit for bit on
+seeded inputs: tensor_silu_*, tensor_rms_norm_*, tensor_layer_norm_*,
+tensor_residual_add_f16 and the softmax inside tensor_sdpa_f32."""
+import numpy as np
+import pytest
+
+from tests.helpers import assert_bits_equal
+
+SHAPES = [(1, 1), (3, 7), (16, 64), (5, 1000), (2, 2048)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_silu(orc, ref, shape, dtype):
+    x = orc.normal(shape, 11, 0, 0.0, 4.0, dtype)
+    assert_bits_equal(orc.silu(x), ref.silu(x), "silu")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("eps", [0.0, 1e-6, 1e-2])
+def test_rms_norm(orc, ref, shape, dtype, eps):
+    x = orc.normal(shape, 12, 0, 0.0, 1.0, dtype)
+    w = orc.uniform(shape[-1:], 12, 1, 0.5, 1.5, dtype)
+    assert_bits_equal(orc.rms_norm(x, w, eps), ref.rms_norm(x, w, eps), "rms_norm")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("affine", ["none", "scale", "both"])
+def test_layer_norm(orc, ref, shape, dtype, affine):
+    x = orc.normal(shape, 13, 0, 0.5, 2.0, dtype)
+    scale = orc.uniform(shape[-1:], 13, 1, 0.5, 1.5, dtype) if affine != "none" else None
+    bias = orc.uniform(shape[-1:], 13, 2, -1.0, 1.0, dtype) if affine == "both" else None
+    assert_bits_equal(orc.layer_norm(x, scale, bias, 1e-5), ref.layer_norm(x, scale, bias, 1e-5),
+                      "layer_norm")
+
+
+@pytest.mark.parametrize("n", [1, 4, 1000, 65536])
+def test_residual_add_f16(orc, ref, n):
+    a = orc.normal((n,), 14, 0, 0.0, 100.0)
+    b = orc.normal((n,), 14, 1, 0.0, 100.0)
+    assert_bits_equal(orc.add(a, b), ref.residual_add_f16(a, b), "residual add")
+
+
+def test_residual_add_f16_all_pairs_sample(orc, ref):
+    """Every half against a fixed set of partners, including specials."""
+    a = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    for partner in (0x0000, 0x8000, 0x3c00, 0x0001, 0x7bff, 0xfbff, 0x7c00, 0x3555):
+        b = np.full(65536, partner, np.uint16).view(np.float16)
+        assert_bits_equal(orc.add(a, b), ref.residual_add_f16(a, b), f"partner {partner:#x}")
+
+
+@pytest.mark.parametrize("q_len,k_len", [(1, 1), (4, 4), (5, 9), (33, 64), (64, 300)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax_via_sdpa(orc, ref, q_len, k_len, causal):
+    s = orc.normal((q_len, k_len), 15, 0, 0.0, 3.0, "f32")
+    assert_bits_equal(orc.softmax(s, causal), ref.softmax_rows_f32(s, causal), "softmax")
+
+
+def test_softmax_special_rows_via_sdpa(orc, ref):
+    """+inf rows, -inf (masked) entries, all -inf rows, huge finite values.
+    NaN scores are not reachable through the reference's public API; the NaN
+    rule is restated from attention.c:346-372 and checked in test_oracle_math."""
+    inf = np.inf
+    s = np.array([[1, 2, inf, 3], [inf, inf, 0, 1], [-inf, -inf, -inf, -inf],
+                  [-inf, 5, -inf, 5], [1e30, -1e30, 0, 1], [-inf, -inf, inf, -inf]], np.float32)
+    for causal in (False, True):
+        assert_bits_equal(orc.softmax(s, causal), ref.softmax_rows_f32(s, causal), "special rows")
