@@ -11,8 +11,8 @@ the kernels run on) for per-kernel durations; the dominant kernel's
 achieved GB/s against the 8 TB/s HBM peak is `roofline`.
 
 The other BASELINE configs are timed per kernel (events around single
-launches, the 256 MB last-level cache flushed between launches) and reported
-under "kernels". The CPU baseline times the oracle (a single-threaded C
+launches, rotating over enough copies of the operands that no launch is
+served from the 256 MB last-level cache) and reported under "suite". The CPU baseline times the oracle (a single-threaded C
 restatement of the reference's portable path) on a bounded slice of the same
 workload.
 
@@ -73,41 +73,42 @@ class Hip:
 
 
 class Timer:
-    """Pairs of events around launches; durations read after the run."""
+    """Events on the SDK stream. `chain` records one marker before the first
+    launch and one after each launch, so consecutive kernels share a marker
+    and each kernel's duration is the gap between its two markers."""
 
     def __init__(self, hip, stream):
-        self.hip, self.stream, self.marks = hip, stream, {}
-        self.pool = []
+        self.hip, self.stream = hip, stream
+        self.pool, self.marks = [], {}
 
     def _event(self):
         return self.pool.pop() if self.pool else self.hip.event()
 
-    def around(self, name, fn):
-        a, b = self._event(), self._event()
-        self.hip.record(a, self.stream)
-        fn()
-        self.hip.record(b, self.stream)
-        self.marks.setdefault(name, []).append((a, b))
+    def chain(self, named_fns):
+        prev = self._event()
+        self.hip.record(prev, self.stream)
+        for name, fn in named_fns:
+            fn()
+            nxt = self._event()
+            self.hip.record(nxt, self.stream)
+            self.marks.setdefault(name, []).append((prev, nxt))
+            prev = nxt
 
     def durations(self):
-        out = {}
+        out, used = {}, set()
         for name, pairs in self.marks.items():
             out[name] = [self.hip.elapsed_ms(a, b) for a, b in pairs]
             for a, b in pairs:
-                self.pool += [a, b]
+                used.update((a, b))
+        self.pool += list(used)
         self.marks = {}
         return out
 
 
-def cfg2_step(sdk, t, timer=None):
-    ops = [("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x_silu"], t["y_silu"])),
-           ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x_gelu"], t["y_gelu"])),
-           ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
-    for name, fn in ops:
-        if timer is None:
-            fn()
-        else:
-            timer.around(name, fn)
+def cfg2_ops(sdk, t):
+    return [("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x_silu"], t["y_silu"])),
+            ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x_gelu"], t["y_gelu"])),
+            ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
 
 
 def cpu_baseline(rows_fraction=4):
@@ -152,107 +153,120 @@ def _cpu_model():
 
 # ---- per-config kernel suite ------------------------------------------------
 
-def suite(sdk, hip, stream, reps=20):
-    """Each BASELINE config's kernels, events around single launches, the
-    last-level cache flushed (512 MiB memset) before every launch."""
-    flush = sdk.tensor("u8", (512 << 20,))
-    flush_ptr = flush.device_ptr()
-    timer = Timer(hip, stream)
-    results = {}
+ROTATE_BYTES = 600 << 20  # traffic between two uses of the same buffers (> 256 MB MALL)
 
-    def measure(name, fn, alg_bytes, elements, warmup=3):
-        for _ in range(warmup):
-            fn()
-        for _ in range(reps):
-            hip.memset(flush_ptr, 512 << 20, stream)
-            timer.around(name, fn)
+
+def suite(sdk, hip, stream, reps=20):
+    """Each BASELINE config's kernels: events around single launches, median
+    of `reps`. Every launch rotates to the next of enough identical copies of
+    its operands that >= 600 MB of other traffic separates two uses of the
+    same bytes, so no operand is served from the 256 MB last-level cache."""
+    from inference_c_amd import TensorView
+    results = {}
+    T = sdk.tensor
+
+    def measure(name, make_set, run, alg_bytes, elements, warmup=3):
+        copies = max(1, -(-ROTATE_BYTES // alg_bytes))
+        sets = [make_set() for _ in range(copies)]
+        for i in range(warmup):
+            run(sets[i % copies])
+        timer = Timer(hip, stream)
+        for i in range(reps):
+            timer.chain([(name, lambda st=sets[i % copies]: run(st))])
         d = timer.durations()[name]
         med = statistics.median(d)
         results[name] = {"median_us": round(med * 1e3, 2), "min_us": round(min(d) * 1e3, 2),
                          "gbps": round(alg_bytes / (med * 1e-3) / 1e9, 1),
                          "pct_peak": round(100 * alg_bytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 1),
                          "elements_per_s": float(f"{elements / (med * 1e-3):.4g}"),
-                         "bytes": alg_bytes}
+                         "bytes": alg_bytes, "buffer_sets": copies}
+        del sets
+        sdk.synchronize()
 
-    T = sdk.tensor
-    # cfg1: f32 add / mul / row-bias add [1024, 4096]
-    a, b, y = T("f32", (1024, 4096)), T("f32", (1024, 4096)), T("f32", (1024, 4096))
-    bias = T("f32", (4096,))
-    sdk.call("tensor_fill_uniform", a, 0, 0, -1.0, 1.0)
-    sdk.call("tensor_fill_uniform", b, 0, 1, -1.0, 1.0)
-    sdk.call("tensor_fill_uniform", bias, 0, 2, -1.0, 1.0)
-    measure("cfg1_add_f32", lambda: sdk.call("tensor_add_f32", a, b, y), 50_331_648, 4_194_304)
-    measure("cfg1_mul_f32", lambda: sdk.call("tensor_mul_f32", a, b, y), 50_331_648, 4_194_304)
-    measure("cfg1_bias_add_f32", lambda: sdk.call("tensor_bias_add_f32", a, bias, y), 33_570_816, 4_194_304)
-    del a, b, y, bias
-    # cfg2
-    x, yy = T("f16", (8192, 8192)), T("f16", (8192, 8192))
-    sdk.call("tensor_fill_normal", x, 1, 0, 0.0, 1.0)
-    measure("cfg2_silu_f16", lambda: sdk.call("tensor_silu_f16", x, yy), *CFG2["silu_f16"])
-    measure("cfg2_gelu_f16", lambda: sdk.call("tensor_gelu_f16", x, yy), *CFG2["gelu_f16"])
-    del x, yy
-    a, b, o = T("f16", (4096, 16384)), T("f16", (4096, 16384)), T("f16", (4096, 16384))
-    sdk.call("tensor_fill_normal", a, 1, 1, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", b, 1, 2, 0.0, 1.0)
-    measure("cfg2_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", b, a, o), *CFG2["swiglu_f16"])
-    del a, b, o
-    # cfg3
-    x, w, y = T("f16", (16384, 2048)), T("f16", (2048,)), T("f16", (16384, 2048))
-    sdk.call("tensor_fill_normal", x, 3, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_uniform", w, 3, 1, 0.5, 1.5)
-    measure("cfg3_rms_norm_f16", lambda: sdk.call("tensor_rms_norm_f16", x, w, 1e-6, y),
-            134_221_824, 33_554_432)
-    del x, w, y
-    lg, pr = T("f16", (32, 2048, 2048)), T("f16", (32, 2048, 2048))
-    sdk.call("tensor_fill_normal", lg, 3, 2, 0.0, 3.0)
-    measure("cfg3_causal_softmax_f16", lambda: sdk.call("tensor_softmax_f16", lg, 1, pr),
-            536_870_912, 134_217_728)
-    del pr
-    rs = T("f32", (32, 2048))
-    measure("cfg3_row_sum_f16", lambda: sdk.call("tensor_row_sum_f16", lg, rs), 268_697_600, 134_217_728)
-    measure("cfg3_row_max_f16", lambda: sdk.call("tensor_row_max_f16", lg, rs), 268_697_600, 134_217_728)
-    del lg, rs
-    # cfg4: (x.permute(0,2,1,3) + A) * M
-    from inference_c_amd import TensorView
+    def filled(dtype, shape, kind, seed, stream_id, a, b):
+        t = T(dtype, shape)
+        sdk.call("tensor_fill_" + kind, t, seed, stream_id, a, b)
+        return t
+
+    # cfg1: f32 add / mul / row-bias add [1024, 4096], U[-1,1], seed 0
+    def cfg1():
+        return (filled("f32", (1024, 4096), "uniform", 0, 0, -1.0, 1.0),
+                filled("f32", (1024, 4096), "uniform", 0, 1, -1.0, 1.0),
+                filled("f32", (4096,), "uniform", 0, 2, -1.0, 1.0), T("f32", (1024, 4096)))
+    measure("cfg1_add_f32", cfg1, lambda s: sdk.call("tensor_add_f32", s[0], s[1], s[3]),
+            50_331_648, 4_194_304)
+    measure("cfg1_mul_f32", cfg1, lambda s: sdk.call("tensor_mul_f32", s[0], s[1], s[3]),
+            50_331_648, 4_194_304)
+    measure("cfg1_bias_add_f32", cfg1, lambda s: sdk.call("tensor_bias_add_f32", s[0], s[2], s[3]),
+            33_570_816, 4_194_304)
+    # cfg2: SiLU / GELU [8192, 8192], SwiGLU [4096, 16384], f16 N(0,1), seed 1
+    def cfg2_unary():
+        return filled("f16", (8192, 8192), "normal", 1, 0, 0.0, 1.0), T("f16", (8192, 8192))
+    measure("cfg2_silu_f16", cfg2_unary, lambda s: sdk.call("tensor_silu_f16", s[0], s[1]),
+            *CFG2["silu_f16"])
+    measure("cfg2_gelu_f16", cfg2_unary, lambda s: sdk.call("tensor_gelu_f16", s[0], s[1]),
+            *CFG2["gelu_f16"])
+    def cfg2_swiglu():
+        return (filled("f16", (4096, 16384), "normal", 1, 1, 0.0, 1.0),
+                filled("f16", (4096, 16384), "normal", 1, 2, 0.0, 1.0), T("f16", (4096, 16384)))
+    measure("cfg2_swiglu_f16", cfg2_swiglu,
+            lambda s: sdk.call("tensor_silu_multiply_f16", s[1], s[0], s[2]), *CFG2["swiglu_f16"])
+    # cfg3: RMSNorm [16384, 2048]; causal softmax / row sum / row max on [32, 2048, 2048]
+    def cfg3_rms():
+        return (filled("f16", (16384, 2048), "normal", 3, 0, 0.0, 1.0),
+                filled("f16", (2048,), "uniform", 3, 1, 0.5, 1.5), T("f16", (16384, 2048)))
+    measure("cfg3_rms_norm_f16", cfg3_rms,
+            lambda s: sdk.call("tensor_rms_norm_f16", s[0], s[1], 1e-6, s[2]), 134_221_824, 33_554_432)
+    def cfg3_logits():
+        return (filled("f16", (32, 2048, 2048), "normal", 3, 2, 0.0, 3.0), T("f16", (32, 2048, 2048)),
+                T("f32", (32, 2048)))
+    measure("cfg3_causal_softmax_f16", cfg3_logits,
+            lambda s: sdk.call("tensor_softmax_f16", s[0], 1, s[1]), 536_870_912, 134_217_728)
+    measure("cfg3_row_sum_f16", cfg3_logits, lambda s: sdk.call("tensor_row_sum_f16", s[0], s[2]),
+            268_697_600, 134_217_728)
+    measure("cfg3_row_max_f16", cfg3_logits, lambda s: sdk.call("tensor_row_max_f16", s[0], s[2]),
+            268_697_600, 134_217_728)
+    # cfg4: (x.permute(0,2,1,3) + A) * M, x [16,1024,32,64]
     B, S, H, D = 16, 1024, 32, 64
-    x, A, M = T("f16", (B, S, H, D)), T("f16", (1, H, 1, D)), T("f16", (B, 1, S, 1))
-    out = T("f16", (B, H, S, D))
-    sdk.call("tensor_fill_normal", x, 4, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_uniform", A, 4, 1, -1.0, 1.0)
-    sdk.call("tensor_fill_uniform", M, 4, 2, -1.0, 1.0)
     view = TensorView.make((B, H, S, D), (S * H * D, D, H * D, 1), 0)
-    measure("cfg4_permuted_broadcast_f16",
-            lambda: sdk.call("tensor_view_add_mul_f16", x, view, A, M, out), 134_254_592, 33_554_432)
-    del x, A, M, out
+    def cfg4():
+        return (filled("f16", (B, S, H, D), "normal", 4, 0, 0.0, 1.0),
+                filled("f16", (1, H, 1, D), "uniform", 4, 1, -1.0, 1.0),
+                filled("f16", (B, 1, S, 1), "uniform", 4, 2, -1.0, 1.0), T("f16", (B, H, S, D)))
+    measure("cfg4_permuted_broadcast_f16", cfg4,
+            lambda s: sdk.call("tensor_view_add_mul_f16", s[0], view, s[1], s[2], s[3]),
+            134_254_592, 33_554_432)
     # cfg5: decoder chain (fused residual+RMSNorm, RoPE q+k, SwiGLU) timed as one chain
     tok, hid, inter = 4096, 2048, 8192
-    x, r, w = T("f16", (tok, hid)), T("f16", (tok, hid)), T("f16", (hid,))
-    h, n = T("f16", (tok, hid)), T("f16", (tok, hid))
-    q, k = T("f16", (tok, 32, 64)), T("f16", (tok, 32, 64))
-    g, u, o = T("f16", (tok, inter)), T("f16", (tok, inter)), T("f16", (tok, inter))
-    for i, t in enumerate((x, r, q, k, g, u)):
-        sdk.call("tensor_fill_normal", t, 5, i, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", w, 5, 9, 0.0, 1.0)
-
-    def chain():
-        sdk.call("tensor_residual_rms_norm_f16", x, r, w, 1e-6, h, n)
-        sdk.call("tensor_rope_f16", q, k, 32, 32, 64, 10000.0, 0)
-        sdk.call("tensor_silu_multiply_f16", g, u, o)
-    measure("cfg5_decoder_chain_f16", chain, 335_548_416, 142_606_336)
-    measure("cfg5_residual_rms_norm_f16",
-            lambda: sdk.call("tensor_residual_rms_norm_f16", x, r, w, 1e-6, h, n), 67_112_960, 8_388_608)
-    measure("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", q, k, 32, 32, 64, 10000.0, 0),
-            67_108_864, 16_777_216)
-    measure("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", g, u, o),
-            201_326_592, 33_554_432)
-    del x, r, w, h, n, q, k, g, u, o
-    big = T("f32", (1 << 30,))
-    sdk.call("tensor_fill_uniform", big, 0, 0, -1.0, 1.0)
-    s64, m32 = T("f64", (1,)), T("f32", (1,))
-    measure("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", big, s64, m32),
-            4_294_967_296, 1_073_741_824)
-    del big
-    sdk.synchronize()
+    def cfg5():
+        return {"x": filled("f16", (tok, hid), "normal", 5, 0, 0.0, 1.0),
+                "r": filled("f16", (tok, hid), "normal", 5, 1, 0.0, 1.0),
+                "w": filled("f16", (hid,), "normal", 5, 9, 0.0, 1.0),
+                "h": T("f16", (tok, hid)), "n": T("f16", (tok, hid)),
+                "q": filled("f16", (tok, 32, 64), "normal", 5, 2, 0.0, 1.0),
+                "k": filled("f16", (tok, 32, 64), "normal", 5, 3, 0.0, 1.0),
+                "g": filled("f16", (tok, inter), "normal", 5, 4, 0.0, 1.0),
+                "u": filled("f16", (tok, inter), "normal", 5, 5, 0.0, 1.0),
+                "o": T("f16", (tok, inter))}
+    def norm(s):
+        sdk.call("tensor_residual_rms_norm_f16", s["x"], s["r"], s["w"], 1e-6, s["h"], s["n"])
+    def rope(s):
+        sdk.call("tensor_rope_f16", s["q"], s["k"], 32, 32, 64, 10000.0, 0)
+    def swiglu(s):
+        sdk.call("tensor_silu_multiply_f16", s["g"], s["u"], s["o"])
+    def chain(s):
+        norm(s)
+        rope(s)
+        swiglu(s)
+    measure("cfg5_decoder_chain_f16", cfg5, chain, 335_548_416, 142_606_336)
+    measure("cfg5_residual_rms_norm_f16", cfg5, norm, 67_112_960, 8_388_608)
+    measure("cfg5_rope_f16", cfg5, rope, 67_108_864, 16_777_216)
+    measure("cfg5_swiglu_f16", cfg5, swiglu, 201_326_592, 33_554_432)
+    # cfg5: global sum + max over 2^30 f32 U[-1,1], seed 0
+    def cfg5_global():
+        return filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0), T("f64", (1,)), T("f32", (1,))
+    measure("cfg5_global_sum_max_f32", cfg5_global,
+            lambda s: sdk.call("tensor_sum_max_f32", s[0], s[1], s[2]), 4_294_967_296, 1_073_741_824)
     return results
 
 
@@ -288,13 +302,15 @@ def main():
     sdk.call("tensor_fill_normal", t["b"], 1, 2, 0.0, 1.0)
     sdk.synchronize()
 
+    ops = cfg2_ops(sdk, t)
     for _ in range(args.warmup):
-        cfg2_step(sdk, t)
+        for _, fn in ops:
+            fn()
     sdk.synchronize()
     timer = Timer(hip, stream)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        cfg2_step(sdk, t, timer)
+        timer.chain(ops)
     sdk.synchronize()
     wall = time.perf_counter() - t0
     per_kernel = {name: sum(d) / len(d) for name, d in timer.durations().items()}

@@ -134,22 +134,24 @@ int host_rope(T *q, T *k, size_t seq, size_t qh, size_t kh, size_t dim, double t
               size_t offset) {
     size_t qn, kn;
     if (q == nullptr || k == nullptr || seq == 0 || qh == 0 || kh == 0 || dim == 0 ||
-        dim % 2 != 0 || dim / 2 > 2048 || qh > (1u << 20) || kh > (1u << 20) ||
+        dim % 2 != 0 || dim > 65536 || qh > (1u << 20) || kh > (1u << 20) ||
         !product(seq, qh * dim, &qn) || !product(seq, kh * dim, &kn) || !count_ok<T>(qn) ||
-        !count_ok<T>(kn))
+        !count_ok<T>(kn) || seq * (dim / 2) > 0xffffffffu)
         return 0;
     Staging st("hip backend", true, nullptr, 0);
     if (!st.begin()) return 0;
     void *pq = st.inout(q, qn * sizeof(T));
     void *pk = st.inout(k, kn * sizeof(T));
     if (st.failed()) return 0;
+    ScratchBlock table(k::rope_table_bytes(seq, dim));
+    if (table.get() == nullptr) return 0;
     hipError_t status;
     if constexpr (sizeof(T) == 4)
         status = k::rope_f32(static_cast<float *>(pq), static_cast<float *>(pk), seq, qh, kh, dim,
-                             theta, offset, st.stream());
+                             theta, offset, table.get(), st.stream());
     else
         status = k::rope_f16(static_cast<uint16_t *>(pq), static_cast<uint16_t *>(pk), seq, qh,
-                             kh, dim, theta, offset, st.stream());
+                             kh, dim, theta, offset, table.get(), st.stream());
     return st.finish(status) ? 1 : 0;
 }
 

@@ -99,21 +99,35 @@ struct RowRegs {
 
     __device__ inline bool valid(int j, uint32_t t, uint32_t vpr) const { return t + j * T < vpr; }
 
+    // Every load is issued unconditionally (a lane past the row end re-reads
+    // vector 0 of the row) and the fill value selected afterwards: a guarded
+    // load becomes a branch after which the compiler waits for it, which
+    // would serialise the row's loads.
     __device__ inline void load(const S *row, uint32_t t, uint32_t vpr, float fill) {
+        Vec16<S> raw[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) raw[j] = load16_stream(row + (size_t)clamp(j, t, vpr) * E);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const uint32_t vi = t + j * T;
-            if (vi < vpr) {
-                const Vec16<S> x = load16_stream(row + (size_t)vi * E);
+            const bool ok = valid(j, t, vpr);
 #pragma unroll
-                for (int e = 0; e < E; ++e) v[j][e] = Elem<S>::load(x.v[e]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) v[j][e] = fill;
-            }
+            for (int e = 0; e < E; ++e) v[j][e] = ok ? Elem<S>::load(raw[j].v[e]) : fill;
         }
     }
+
+    __device__ static inline uint32_t clamp(int j, uint32_t t, uint32_t vpr) {
+        const uint32_t vi = t + j * T;
+        return vi < vpr ? vi : 0u;
+    }
 };
+
+// Unconditional loads of a per-column parameter slice (weights, scale, bias).
+template <typename S, int NV, int WPR>
+__device__ inline void load_params(const S *p, uint32_t t, uint32_t vpr, Vec16<S> (&out)[NV]) {
+    using R = RowRegs<S, NV, WPR>;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) out[j] = load16(p + (size_t)R::clamp(j, t, vpr) * R::E);
+}
 
 // ---- RMSNorm / fused residual + RMSNorm ------------------------------------
 
@@ -130,20 +144,24 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
     const size_t base = slot.row * width;
     R r;
     r.load(x + base, slot.t, vpr, 0.0f);
+    // the weight slice is fetched (from L2) while the row is still in flight
+    Vec16<S> wv[NV];
+    load_params<S, NV, WPR>(w, slot.t, vpr, wv);
     if constexpr (kResidual) {
+        Vec16<S> rv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            rv[j] = load16_stream(residual + base + (size_t)R::clamp(j, slot.t, vpr) * E);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const uint32_t vi = slot.t + j * R::T;
-            if (vi < vpr) {
-                const Vec16<S> rv = load16_stream(residual + base + (size_t)vi * E);
-                Vec16<S> sum;
+            Vec16<S> sum;
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    sum.v[e] = Elem<S>::store(r.v[j][e] + Elem<S>::load(rv.v[e]));
-                    r.v[j][e] = Elem<S>::load(sum.v[e]);
-                }
-                store16_stream(sum_out + base + (size_t)vi * E, sum);
+            for (int e = 0; e < E; ++e) {
+                sum.v[e] = Elem<S>::store(r.v[j][e] + Elem<S>::load(rv[j].v[e]));
+                r.v[j][e] = vi < vpr ? Elem<S>::load(sum.v[e]) : 0.0f;
             }
+            if (vi < vpr) store16_stream(sum_out + base + (size_t)vi * E, sum);
         }
     }
     float squares = 0.0f;
@@ -157,11 +175,10 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
         if (vi < vpr) {
-            const Vec16<S> wv = load16(w + (size_t)vi * E);
             Vec16<S> out;
 #pragma unroll
             for (int e = 0; e < E; ++e)
-                out.v[e] = Elem<S>::store(r.v[j][e] * scale * Elem<S>::load(wv.v[e]));
+                out.v[e] = Elem<S>::store(r.v[j][e] * scale * Elem<S>::load(wv[j].v[e]));
             store16_stream(y + base + (size_t)vi * E, out);
         }
     }
@@ -207,6 +224,9 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
     const size_t base = slot.row * width;
     R r;
     r.load(x + base, slot.t, vpr, 0.0f);
+    Vec16<S> sv[NV], bv[NV];
+    if (scale) load_params<S, NV, WPR>(scale, slot.t, vpr, sv);
+    if (bias) load_params<S, NV, WPR>(bias, slot.t, vpr, bv);
     float total = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -229,15 +249,12 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
         if (vi < vpr) {
-            Vec16<S> sv{}, bv{};
-            if (scale) sv = load16(scale + (size_t)vi * E);
-            if (bias) bv = load16(bias + (size_t)vi * E);
             Vec16<S> out;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float v = (r.v[j][e] - mean) * inverse_std;
-                if (scale) v *= Elem<S>::load(sv.v[e]);
-                if (bias) v += Elem<S>::load(bv.v[e]);
+                if (scale) v *= Elem<S>::load(sv[j].v[e]);
+                if (bias) v += Elem<S>::load(bv[j].v[e]);
                 out.v[e] = Elem<S>::store(v);
             }
             store16_stream(y + base + (size_t)vi * E, out);
@@ -302,23 +319,26 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     R r;
     float m = neg_inf;
     int pos_inf = 0;
+    // Vectors entirely past the causal limit re-read the row's first vector
+    // (already requested by lane 0, so no HBM traffic) instead of branching.
+    Vec16<S> raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
-        const uint64_t first = (uint64_t)vi * E;
-        if (vi < vpr && first <= limit) {
-            const Vec16<S> xv = load16_stream(x + base + first);
+        const bool use = vi < vpr && (uint64_t)vi * E <= limit;
+        raw[j] = load16_stream(x + base + (size_t)(use ? vi : 0u) * E);
+    }
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                float s = Elem<S>::load(xv.v[e]);
-                s = first + e <= limit ? s : neg_inf;
-                r.v[j][e] = s;
-                m = fmaxf(m, s);
-                pos_inf += s == __builtin_inff();
-            }
-        } else {
+    for (int j = 0; j < NV; ++j) {
+        const uint64_t first = (uint64_t)(slot.t + j * R::T) * E;
+        const bool row_ok = slot.t + j * R::T < vpr;
 #pragma unroll
-            for (int e = 0; e < E; ++e) r.v[j][e] = neg_inf;
+        for (int e = 0; e < E; ++e) {
+            float s = Elem<S>::load(raw[j].v[e]);
+            s = row_ok && first + e <= limit ? s : neg_inf;
+            r.v[j][e] = s;
+            m = fmaxf(m, s);
+            pos_inf += s == __builtin_inff();
         }
     }
     m = group_max<WPR>(m, lds);

@@ -2,7 +2,7 @@
 //     y[i] = (x[view(i)] + addend[bcast(i)]) * mult[bcast(i)]
 // with y contiguous in the view's shape.
 //
-// Three paths, chosen on the host from the strides:
+// Four paths, chosen on the host from the strides:
 //   vector  - the view's last dimension is contiguous in x (stride 1) and all
 //             offsets are multiples of the 16-byte vector: every lane
 //             decomposes its output-vector index with multiply-high
@@ -10,6 +10,10 @@
 //             innermost dimension), applies the broadcast operands (a vector
 //             when the operand spans the last dimension, a scalar when it is
 //             broadcast along it) and stores 16 bytes;
+//   vector tile - as vector, but the output dim next to the last one is not
+//             adjacent to it in x while another dim is (a permutation such as
+//             (0,2,1,3)): 8x8 tiles of contiguous runs are transposed through
+//             LDS so that reads and writes are both contiguous 8-run rows;
 //   tile    - x's contiguous dimension is another view dimension p (a
 //             transpose of p with the last dimension): 64x64 tiles are read
 //             along p, staged through LDS (padded against bank conflicts) and
@@ -192,6 +196,131 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
     }
 }
 
+// ---- LDS-staged vector tile path ----------------------------------------------
+
+// For views whose last dimension L is contiguous in x and in the output but
+// whose next-outer output dimension o is not adjacent to L in x, while some
+// other dimension t is (x stride of t == L): e.g. a (0,2,1,3) permutation.
+// A block moves an 8 x 8 tile of (o, t) "units" (one unit = the L contiguous
+// elements, kVpu 16-byte vectors): it reads the tile as 8 rows of 8
+// x-contiguous units, stages them in LDS, and writes 8 rows of 8
+// output-contiguous units, so both HBM streams are contiguous runs of
+// 8 * L elements. LDS rows are padded by 128 bytes so that the 16-lane
+// phases of ds_read_b128 fall on disjoint banks when kVpu = 8.
+constexpr int kTileUnits = 8;
+
+struct TileVecPlan {
+    int rank;
+    int o, t;                       // tiled dims (o = rank - 2)
+    uint64_t shape[kMaxRank];
+    int64_t x_stride[kMaxRank];
+    uint64_t a_stride[kMaxRank];
+    uint64_t m_stride[kMaxRank];
+    uint64_t y_stride[kMaxRank];
+    uint64_t x_offset;
+    uint32_t tiles_o, tiles_t;
+    int a_vec, m_vec;
+};
+
+template <typename S, int kVpu>
+__global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(const S *__restrict__ x,
+                                                               const S *__restrict__ addend,
+                                                               const S *__restrict__ mult,
+                                                               S *__restrict__ y,
+                                                               TileVecPlan plan) {
+    constexpr int E = Vec16<S>::N;
+    constexpr int kRow = kTileUnits * kVpu + 8;  // vectors per LDS row (padded)
+    constexpr int kVecs = kTileUnits * kTileUnits * kVpu;
+    __shared__ Vec16<S> lds[kTileUnits * kRow];
+    const int last = plan.rank - 1;
+    const uint64_t block = blockIdx.x;
+    const uint32_t bt = (uint32_t)(block % plan.tiles_t);
+    const uint32_t bo = (uint32_t)((block / plan.tiles_t) % plan.tiles_o);
+    uint64_t batch = block / ((uint64_t)plan.tiles_t * plan.tiles_o);
+    int64_t xb = (int64_t)plan.x_offset;
+    uint64_t ab = 0, mb = 0, yb = 0;
+    for (int d = last - 1; d >= 0; --d) {
+        if (d == plan.o || d == plan.t) continue;
+        const uint64_t idx = batch % plan.shape[d];
+        batch /= plan.shape[d];
+        xb += (int64_t)idx * plan.x_stride[d];
+        ab += idx * plan.a_stride[d];
+        mb += idx * plan.m_stride[d];
+        yb += idx * plan.y_stride[d];
+    }
+    const uint64_t o0 = (uint64_t)bo * kTileUnits, t0 = (uint64_t)bt * kTileUnits;
+    const uint64_t no = plan.shape[plan.o], nt = plan.shape[plan.t];
+    constexpr int kPer = (kVecs + kBlock - 1) / kBlock;  // vectors per thread per phase
+    // read: o-rows of t-contiguous units (all of this thread's loads in flight)
+    Vec16<S> xin[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int v = threadIdx.x + u * kBlock;
+        const int oi = v / (kTileUnits * kVpu);
+        const int rem = v - oi * (kTileUnits * kVpu);
+        const int ti = rem / kVpu, c = rem - ti * kVpu;
+        const bool ok = v < kVecs && o0 + oi < no && t0 + ti < nt;
+        xin[u] = load16_stream(x + (ok ? xb + (int64_t)(o0 + oi) * plan.x_stride[plan.o] +
+                                              (int64_t)(t0 + ti) * plan.x_stride[plan.t] + c * E
+                                         : xb));
+    }
+    // the write phase's broadcast operands are fetched before the barrier
+    Vec16<S> av[kPer], mv[kPer];
+    float as[kPer], ms[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int v = threadIdx.x + u * kBlock;
+        const int ti = v / (kTileUnits * kVpu);
+        const int rem = v - ti * (kTileUnits * kVpu);
+        const int oi = rem / kVpu, c = rem - oi * kVpu;
+        const bool ok = v < kVecs && o0 + oi < no && t0 + ti < nt;
+        as[u] = 0.0f;
+        ms[u] = 1.0f;
+        if (addend) {
+            const uint64_t ao = ok ? ab + (t0 + ti) * plan.a_stride[plan.t] +
+                                         (o0 + oi) * plan.a_stride[plan.o] : 0;
+            if (plan.a_vec) av[u] = load16(addend + ao + (ok ? (uint64_t)c * E : 0));
+            else as[u] = Elem<S>::load(addend[ao]);
+        }
+        if (mult) {
+            const uint64_t mo = ok ? mb + (t0 + ti) * plan.m_stride[plan.t] +
+                                         (o0 + oi) * plan.m_stride[plan.o] : 0;
+            if (plan.m_vec) mv[u] = load16(mult + mo + (ok ? (uint64_t)c * E : 0));
+            else ms[u] = Elem<S>::load(mult[mo]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int v = threadIdx.x + u * kBlock;
+        const int oi = v / (kTileUnits * kVpu);
+        const int rem = v - oi * (kTileUnits * kVpu);
+        const int ti = rem / kVpu, c = rem - ti * kVpu;
+        if (v < kVecs) lds[oi * kRow + ti * kVpu + c] = xin[u];
+    }
+    __syncthreads();
+    // write: t-rows of o-contiguous units
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int v = threadIdx.x + u * kBlock;
+        const int ti = v / (kTileUnits * kVpu);
+        const int rem = v - ti * (kTileUnits * kVpu);
+        const int oi = rem / kVpu, c = rem - oi * kVpu;
+        if (v >= kVecs || o0 + oi >= no || t0 + ti >= nt) continue;
+        const Vec16<S> xv = lds[oi * kRow + ti * kVpu + c];
+        Vec16<S> out;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            float r = Elem<S>::load(xv.v[e]);
+            if (addend) r = r + (plan.a_vec ? Elem<S>::load(av[u].v[e]) : as[u]);
+            if (mult) r = r * (plan.m_vec ? Elem<S>::load(mv[u].v[e]) : ms[u]);
+            out.v[e] = Elem<S>::store(r);
+        }
+        store16_stream(y + yb + (t0 + ti) * plan.y_stride[plan.t] +
+                           (o0 + oi) * plan.y_stride[plan.o] + (uint64_t)c * E,
+                       out);
+    }
+}
+
 inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
 // Contiguous strides of a broadcast operand, zeroed where its dim is 1.
@@ -227,6 +356,50 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend, const 
     for (int d = 0; d < last && vec; ++d) {
         if (a_vec) vec = a_stride[d] % E == 0;
         if (vec && m_vec) vec = m_stride[d] % E == 0;
+    }
+    // LDS tile path: o = rank-2 is not next to the last dim in x but some
+    // other dim t is (x stride == L); both streams become contiguous runs.
+    if (vec && rank >= 3) {
+        const int o = rank - 2;
+        const int64_t L = (int64_t)v.shape[last];
+        int t = -1;
+        for (int d = 0; d < last; ++d)
+            if (d != o && v.strides[d] == L && v.shape[d] > 1) t = d;
+        const uint64_t vpu = v.shape[last] / E;
+        if (t >= 0 && v.strides[o] != L && v.shape[o] > 1 &&
+            (vpu == 1 || vpu == 2 || vpu == 4 || vpu == 8 || vpu == 16)) {
+            TileVecPlan plan{};
+            plan.rank = rank;
+            plan.o = o;
+            plan.t = t;
+            uint64_t ys = 1;
+            for (int d = last; d >= 0; --d) {
+                plan.shape[d] = v.shape[d];
+                plan.x_stride[d] = v.strides[d];
+                plan.a_stride[d] = a_stride[d];
+                plan.m_stride[d] = m_stride[d];
+                plan.y_stride[d] = ys;
+                ys *= v.shape[d];
+            }
+            plan.x_offset = v.offset;
+            plan.tiles_o = (uint32_t)((v.shape[o] + kTileUnits - 1) / kTileUnits);
+            plan.tiles_t = (uint32_t)((v.shape[t] + kTileUnits - 1) / kTileUnits);
+            plan.a_vec = a_vec;
+            plan.m_vec = m_vec;
+            const uint64_t batches = n / (v.shape[o] * v.shape[t] * v.shape[last]);
+            const uint64_t blocks = batches * plan.tiles_o * plan.tiles_t;
+            if (blocks < (uint64_t{1} << 31)) {
+                const dim3 grid((unsigned)blocks), block(kBlock);
+                switch (vpu) {
+                    case 1: hipLaunchKernelGGL((view_tile_vec_kernel<S, 1>), grid, block, 0, s, x, addend, mult, y, plan); break;
+                    case 2: hipLaunchKernelGGL((view_tile_vec_kernel<S, 2>), grid, block, 0, s, x, addend, mult, y, plan); break;
+                    case 4: hipLaunchKernelGGL((view_tile_vec_kernel<S, 4>), grid, block, 0, s, x, addend, mult, y, plan); break;
+                    case 8: hipLaunchKernelGGL((view_tile_vec_kernel<S, 8>), grid, block, 0, s, x, addend, mult, y, plan); break;
+                    default: hipLaunchKernelGGL((view_tile_vec_kernel<S, 16>), grid, block, 0, s, x, addend, mult, y, plan); break;
+                }
+                return hipGetLastError();
+            }
+        }
     }
     if (vec) {
         ViewPlan plan{};

@@ -69,11 +69,14 @@ hipError_t argmax_f32(const float *x, size_t n, uint32_t *index_out, void *parti
 hipError_t argmax_f16(const uint16_t *x, size_t n, uint32_t *index_out, void *partials,
                       hipStream_t s);
 
-// In-place split-half RoPE on q [seq, qh, dim] and k [seq, kh, dim].
+// In-place split-half RoPE on q [seq, qh, dim] and k [seq, kh, dim]. `table`
+// is device scratch of rope_table_bytes(seq, dim) bytes (the per-call
+// cos/sin table).
+size_t rope_table_bytes(size_t seq, size_t dim);
 hipError_t rope_f32(float *q, float *k, size_t seq, size_t qh, size_t kh, size_t dim,
-                    double theta, size_t offset, hipStream_t s);
+                    double theta, size_t offset, void *table, hipStream_t s);
 hipError_t rope_f16(uint16_t *q, uint16_t *k, size_t seq, size_t qh, size_t kh,
-                    size_t dim, double theta, size_t offset, hipStream_t s);
+                    size_t dim, double theta, size_t offset, void *table, hipStream_t s);
 
 // Strided view (x + addend) * mult -> contiguous y. Shapes/strides in
 // elements; addend/mult shapes broadcast (1 or equal), either may be null.

@@ -329,13 +329,14 @@ int argmax(TensorDType dtype, Buf x, TensorBuffer *index, char *error, size_t ca
 int rope(TensorDType dtype, TensorBuffer *q, TensorBuffer *k, size_t qh, size_t kh,
          size_t dim, double theta, size_t offset, char *error, size_t capacity) {
     const size_t qn = tensor_buffer_element_count(q), kn = tensor_buffer_element_count(k);
-    const bool shape_ok = qh > 0 && kh > 0 && dim > 0 && dim % 2 == 0 && dim / 2 <= 2048 &&
+    const bool shape_ok = qh > 0 && kh > 0 && dim > 0 && dim % 2 == 0 && dim <= 65536 &&
                           qh <= (1u << 20) && kh <= (1u << 20) && qn % (qh * dim) == 0 &&
-                          kn == qn / (qh * dim) * kh * dim;
+                          kn == qn / (qh * dim) * kh * dim &&
+                          qn / (qh * dim) * (dim / 2) <= 0xffffffffu;
     if (!is(q, dtype) || !is(k, dtype) || !shape_ok || !std::isfinite(theta) || theta <= 0.0) {
         set_error(error, capacity,
                   "RoPE requires %s query [seq, query_heads, head_dim] and key [seq, "
-                  "key_heads, head_dim] with an even head_dim <= 4096 and a finite positive "
+                  "key_heads, head_dim] with an even head_dim <= 65536 and a finite positive "
                   "theta", dtype == TENSOR_DTYPE_F32 ? "F32" : "F16");
         return 0;
     }
@@ -348,12 +349,17 @@ int rope(TensorDType dtype, TensorBuffer *q, TensorBuffer *k, size_t qh, size_t 
     void *pq = srcdst(st, q);
     void *pk = srcdst(st, k);
     if (st.failed()) return 0;
+    ScratchBlock table(k::rope_table_bytes(seq, dim));
+    if (table.get() == nullptr) {
+        set_error(error, capacity, "RoPE: out of device memory for the angle table");
+        return 0;
+    }
     const hipError_t status =
         dtype == TENSOR_DTYPE_F32
             ? k::rope_f32(as<float>(pq), as<float>(pk), seq, qh, kh, dim, theta, offset,
-                          st.stream())
+                          table.get(), st.stream())
             : k::rope_f16(as<uint16_t>(pq), as<uint16_t>(pk), seq, qh, kh, dim, theta, offset,
-                          st.stream());
+                          table.get(), st.stream());
     return st.finish(status) ? 1 : 0;
 }
 

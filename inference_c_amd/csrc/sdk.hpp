@@ -33,6 +33,22 @@ void *scratch_acquire(size_t bytes);
 void scratch_release(void *ptr, size_t bytes);
 void scratch_clear();
 
+// A pool block held for the duration of one call. Returning it to the pool
+// right after the launches is safe: every later user of the block enqueues
+// on the same SDK stream, after this call's kernels.
+class ScratchBlock {
+public:
+    explicit ScratchBlock(size_t bytes) : bytes_(bytes == 0 ? 1 : bytes), ptr_(scratch_acquire(bytes_)) {}
+    ScratchBlock(const ScratchBlock &) = delete;
+    ScratchBlock &operator=(const ScratchBlock &) = delete;
+    ~ScratchBlock() { scratch_release(ptr_, bytes_); }
+    void *get() const { return ptr_; }
+
+private:
+    size_t bytes_;
+    void *ptr_;
+};
+
 // Partial-result buffer of the two-pass grid reductions. The launches of one
 // reduction must be enqueued under grid_reduce_mutex() so that two host
 // threads never interleave their passes on the shared buffer.

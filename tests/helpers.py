@@ -79,3 +79,15 @@ def arbitrated(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, ulps) -> np.
     r = ref.astype(np.float64)
     closer = np.abs(g - exact) <= np.abs(r - exact)
     return within | closer
+
+
+def rope_close(got, want, src):
+    """RoPE f16 rule: 1 f16 ulp, or -- where l*c - r*s cancels -- the f32
+    error of a rotation whose cos/sin are each within an f32 ulp of the
+    reference's: 2^-22 (|l| + |r|)."""
+    half = src.shape[-1] // 2
+    pair = np.abs(src[..., :half].astype(np.float64)) + np.abs(src[..., half:].astype(np.float64))
+    pair = np.concatenate([pair, pair], axis=-1)
+    d = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    ok = (f16_ulps(got, want) <= 1) | (d <= 2.0 ** -22 * pair)
+    assert ok.all(), f"{(~ok).sum()} elements beyond the RoPE bound"

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from inference_c_amd import TensorView
-from tests.helpers import assert_bits_equal, assert_f16_ulps
+from tests.helpers import assert_bits_equal, assert_f16_ulps, rope_close
 
 pytestmark = pytest.mark.gpu
 F16 = np.float16
@@ -23,8 +23,8 @@ def test_rope_f16(sdk, orc, seq, qh, kh, dim, offset, device):
     tq, tk = sdk.from_numpy(q, device=device), sdk.from_numpy(k, device=device)
     sdk.call("tensor_rope_f16", tq, tk, qh, kh, dim, 10000.0, offset)
     wq, wk = orc.rope(q, k, qh, kh, dim, 10000.0, offset)
-    assert_f16_ulps(tq.download(), wq, 1, "rope q")
-    assert_f16_ulps(tk.download(), wk, 1, "rope k")
+    rope_close(tq.download(), wq, q)
+    rope_close(tk.download(), wk, k)
 
 
 @pytest.mark.parametrize("seq,qh,kh,dim,offset", [(64, 4, 2, 64, 0), (7, 3, 3, 10, 77)])
@@ -81,15 +81,28 @@ def test_config4_permuted_broadcast(sdk, orc, device):
     view_case(sdk, orc, x, (B, H, S, D), (S * H * D, D, H * D, 1), 0, A, M, device=device)
 
 
-@pytest.mark.parametrize("case", ["vector", "tile", "scalar", "broadcast_x", "offset", "rank1"])
+@pytest.mark.parametrize("case", ["vector_tile", "vector_tile_ragged", "vector_rows", "tile",
+                                  "scalar", "broadcast_x", "offset", "rank1"])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_view_paths(sdk, orc, case, dtype):
     dt = "f16" if dtype == "f16" else "f32"
-    if case == "vector":       # last dim contiguous
+    if case == "vector_tile":  # (0,2,1,3) permutation: LDS-staged 8x8 unit tiles
         x = orc.normal((3, 40, 5, 16), 52, 0, 0.0, 1.0, dt)
         shape, strides, off = (3, 5, 40, 16), (3200, 16, 80, 1), 0
         A = orc.uniform((1, 5, 1, 16), 52, 1, -1, 1, dt)
         M = orc.uniform((3, 1, 40, 1), 52, 2, -1, 1, dt)
+    elif case == "vector_tile_ragged":  # tile edges (13, 11 not multiples of 8), batch dims
+        x = orc.normal((2, 3, 13, 11, 32), 58, 0, 0.0, 1.0, dt)
+        shape = (2, 3, 11, 13, 32)
+        strides = (3 * 13 * 11 * 32, 13 * 11 * 32, 32, 11 * 32, 1)
+        off = 0
+        A = orc.uniform((1, 3, 11, 1, 32), 58, 1, -1, 1, dt)
+        M = orc.uniform((2, 1, 1, 13, 1), 58, 2, -1, 1, dt)
+    elif case == "vector_rows":  # strided rows, last dim contiguous, no tile partner
+        x = orc.normal((4, 6, 16), 59, 0, 0.0, 1.0, dt)
+        shape, strides, off = (4, 3, 16), (96, 32, 1), 0
+        A = orc.uniform((4, 3, 16), 59, 1, -1, 1, dt)
+        M = orc.uniform((1, 3, 1), 59, 2, -1, 1, dt)
     elif case == "tile":       # transpose of the last two dims
         x = orc.normal((2, 3, 70, 130), 53, 0, 0.0, 1.0, dt)
         shape, strides, off = (2, 3, 130, 70), (3 * 70 * 130, 70 * 130, 1, 130), 0

@@ -144,12 +144,20 @@ def test_softmax_special_rows(sdk, orc, dtype, width):
 
 
 def test_softmax_first_causal_row_is_one(sdk, orc):
-    x = orc.normal((2, 128, 2048), 28, 0, 0.0, 3.0)
+    """Square causal block (q_len == k_len, so the causal offset is 0)."""
+    x = orc.normal((2, 256, 256), 28, 0, 0.0, 3.0)
     tx, ty = sdk.from_numpy(x), sdk.tensor("f16", x.shape)
     sdk.call("tensor_softmax_f16", tx, 1, ty)
     y = ty.download()
     assert np.all(y[:, 0, 0] == 1) and np.all(y[:, 0, 1:] == 0)
     assert np.all(np.triu(y[0].astype(np.float32), 1) == 0)
+    # q_len < k_len aligns the mask to the end (attention.c causal_offset):
+    # query row 0 sees keys 0..k_len-q_len
+    x = orc.normal((1, 4, 64), 28, 1, 0.0, 3.0)
+    tx, ty = sdk.from_numpy(x), sdk.tensor("f16", x.shape)
+    sdk.call("tensor_softmax_f16", tx, 1, ty)
+    y = ty.download()[0].astype(np.float32)
+    assert np.all(y[0, 61:] == 0) and np.all(y[0, :61] > 0) and np.all(y[3] > 0)
 
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])

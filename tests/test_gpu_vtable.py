@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from tests.helpers import arbitrated, assert_bits_equal, assert_f16_ulps, assert_f32_rel, f16_ulps
+from tests.helpers import arbitrated, assert_bits_equal, assert_f16_ulps, f16_ulps, rope_close
 
 pytestmark = pytest.mark.gpu
 
@@ -154,10 +154,11 @@ def test_slots_vs_oracle(hip, orc):
     seq, heads, dim = 50, 4, 64
     q = orc.normal((seq, heads, dim), 60, 5, 0.0, 1.0)
     k = orc.normal((seq, 2, dim), 60, 6, 0.0, 1.0)
+    q0, k0 = q.copy(), k.copy()
     wq, wk = orc.rope(q, k, heads, 2, dim, 10000.0, 7)
     assert hip["rope_f16"](p(q), p(k), seq, heads, 2, dim, 10000.0, 7)
-    assert_f16_ulps(q, wq, 1, "rope slot q")
-    assert_f16_ulps(k, wk, 1, "rope slot k")
+    rope_close(q, wq, q0)
+    rope_close(k, wk, k0)
     hip["table"].release_cache and ctypes.CFUNCTYPE(None)(hip["table"].release_cache)()
 
 
