@@ -270,6 +270,38 @@ def suite(sdk, hip, stream, reps=20):
     return results
 
 
+COPY_BYTES = 256 << 20  # calibration copy for counter runs: 256 MiB read + 256 MiB written
+
+
+def pmc_probe(sdk, reps=3):
+    """Workload for `rocprofv3 --pmc` runs: a plain 16-byte-vector copy of
+    COPY_BYTES (known traffic, the calibration for FETCH_SIZE / WRITE_SIZE),
+    then each cfg2 kernel, `reps` times each, with a 600 MB cache-flushing
+    write between dispatches so that every dispatch starts from HBM."""
+    from inference_c_amd import TensorView
+    n = COPY_BYTES // 2
+    src, dst = sdk.tensor("f16", (n,)), sdk.tensor("f16", (n,))
+    flush = sdk.tensor("f32", (ROTATE_BYTES // 4,))
+    sdk.call("tensor_fill_normal", src, 1, 9, 0.0, 1.0)
+    t = {}
+    t["x"], t["y"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
+    t["a"], t["b"], t["o"] = (sdk.tensor("f16", (4096, 16384)) for _ in range(3))
+    sdk.call("tensor_fill_normal", t["x"], 1, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["a"], 1, 1, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["b"], 1, 2, 0.0, 1.0)
+    view = TensorView.make((n,), (1,), 0)
+    ops = [("copy_f16", lambda: sdk.call("tensor_view_add_mul_f16", src, view, None, None, dst)),
+           ("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x"], t["y"])),
+           ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x"], t["y"])),
+           ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
+    for name, fn in ops:
+        for _ in range(reps):
+            sdk.call("tensor_fill_uniform", flush, 7, 0, -1.0, 1.0)
+            fn()
+            sdk.synchronize()
+        print(f"pmc probe: {name} x{reps}", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -277,6 +309,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only run the counter-collection workload (copy + cfg2 kernels)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one "
@@ -287,6 +321,9 @@ def main():
     from inference_c_amd import Sdk
     sdk = Sdk()
     sdk.require_device()
+    if args.pmc_probe:
+        pmc_probe(sdk)
+        return
     hip = Hip()
     stream = sdk.stream()
 
