@@ -5,14 +5,15 @@ Step: one pass of the FP16 unary/fused elementwise
 workload -- SiLU and tanh-GELU on [8192, 8192] f16 N(0,1) and SwiGLU
 out = a * silu(b) on [4096, 16384] f16 N(0,1), seed 1 -- with every input
 already resident in HBM. `value` is the step's algorithmic bytes (each input
-read once, each output written once) over the wall time of K steps. Every
-kernel launch is also bracketed by HIP events on the SDK stream (the stream
-the kernels run on) for per-kernel durations; the dominant kernel's
-achieved GB/s against the 8 TB/s HBM peak is `roofline`.
+read once, each output written once) over the wall time of K steps. The K
+launches of each kernel run back to back between HIP events on the SDK
+stream (the stream the kernels run on), which gives each kernel's average
+launch duration; the dominant kernel's achieved GB/s against the 8 TB/s HBM
+peak is `roofline`. Operands rotate over enough identical copies that no
+launch is served from the 256 MB last-level cache.
 
-The other BASELINE configs are timed per kernel (events around single
-launches, rotating over enough copies of the operands that no launch is
-served from the 256 MB last-level cache) and reported under "suite". The CPU baseline times the oracle (a single-threaded C
+The other BASELINE configs are timed per kernel the same way and reported
+under "suite". The CPU baseline times the oracle (a single-threaded C
 restatement of the reference's portable path) on a bounded slice of the same
 workload.
 
@@ -72,43 +73,23 @@ class Hip:
         assert self.lib.hipMemsetAsync(ptr, 0, nbytes, stream) == 0
 
 
-class Timer:
-    """Events on the SDK stream. `chain` records one marker before the first
-    launch and one after each launch, so consecutive kernels share a marker
-    and each kernel's duration is the gap between its two markers."""
-
-    def __init__(self, hip, stream):
-        self.hip, self.stream = hip, stream
-        self.pool, self.marks = [], {}
-
-    def _event(self):
-        return self.pool.pop() if self.pool else self.hip.event()
-
-    def chain(self, named_fns):
-        prev = self._event()
-        self.hip.record(prev, self.stream)
-        for name, fn in named_fns:
-            fn()
-            nxt = self._event()
-            self.hip.record(nxt, self.stream)
-            self.marks.setdefault(name, []).append((prev, nxt))
-            prev = nxt
-
-    def durations(self):
-        out, used = {}, set()
-        for name, pairs in self.marks.items():
-            out[name] = [self.hip.elapsed_ms(a, b) for a, b in pairs]
-            for a, b in pairs:
-                used.update((a, b))
-        self.pool += list(used)
-        self.marks = {}
-        return out
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "cfg2_hbm_traffic.md")
 
 
-def cfg2_ops(sdk, t):
-    return [("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x_silu"], t["y_silu"])),
-            ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x_gelu"], t["y_gelu"])),
-            ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (lines `traffic_bytes <kernel> <bytes>`: FETCH_SIZE and WRITE_SIZE of
+    two rocprofv3 --pmc runs, each scaled by the same counter's reading for a
+    copy of known size), or None when the summary has no line for it."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(rows_fraction=4):
@@ -156,11 +137,13 @@ def _cpu_model():
 ROTATE_BYTES = 600 << 20  # traffic between two uses of the same buffers (> 256 MB MALL)
 
 
-def suite(sdk, hip, stream, reps=20):
-    """Each BASELINE config's kernels: events around single launches, median
-    of `reps`. Every launch rotates to the next of enough identical copies of
-    its operands that >= 600 MB of other traffic separates two uses of the
-    same bytes, so no operand is served from the 256 MB last-level cache."""
+def suite(sdk, hip, stream, reps=20, rounds=3):
+    """Each BASELINE config's kernels: `reps` back-to-back launches between
+    two events on the SDK stream, average per launch; the best of `rounds`
+    such batches is reported with all of them. Every launch rotates to the
+    next of enough identical copies of its operands that >= 600 MB of other
+    traffic separates two uses of the same bytes, so no operand is served
+    from the 256 MB last-level cache."""
     from inference_c_amd import TensorView
     results = {}
     T = sdk.tensor
@@ -170,15 +153,20 @@ def suite(sdk, hip, stream, reps=20):
         sets = [make_set() for _ in range(copies)]
         for i in range(warmup):
             run(sets[i % copies])
-        timer = Timer(hip, stream)
-        for i in range(reps):
-            timer.chain([(name, lambda st=sets[i % copies]: run(st))])
-        d = timer.durations()[name]
-        med = statistics.median(d)
-        results[name] = {"median_us": round(med * 1e3, 2), "min_us": round(min(d) * 1e3, 2),
-                         "gbps": round(alg_bytes / (med * 1e-3) / 1e9, 1),
-                         "pct_peak": round(100 * alg_bytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 1),
-                         "elements_per_s": float(f"{elements / (med * 1e-3):.4g}"),
+        start, stop = hip.event(), hip.event()
+        batches = []
+        for _ in range(rounds):
+            hip.record(start, stream)
+            for i in range(reps):
+                run(sets[i % copies])
+            hip.record(stop, stream)
+            batches.append(hip.elapsed_ms(start, stop) / reps)
+        best = min(batches)
+        results[name] = {"avg_us": round(best * 1e3, 2),
+                         "batches_us": [round(t * 1e3, 2) for t in batches],
+                         "gbps": round(alg_bytes / (best * 1e-3) / 1e9, 1),
+                         "pct_peak": round(100 * alg_bytes / (best * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                         "elements_per_s": float(f"{elements / (best * 1e-3):.4g}"),
                          "bytes": alg_bytes, "buffer_sets": copies}
         del sets
         sdk.synchronize()
@@ -305,8 +293,8 @@ def pmc_probe(sdk, reps=3):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -327,30 +315,47 @@ def main():
     hip = Hip()
     stream = sdk.stream()
 
-    t = {}
-    t["x_silu"], t["y_silu"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
-    t["x_gelu"], t["y_gelu"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
-    t["a"], t["b"], t["o"] = (sdk.tensor("f16", (4096, 16384)) for _ in range(3))
-    # separate (identical) SiLU and GELU inputs: the step touches 896 MiB, so
-    # no input is still in the 256 MB last-level cache when it is read again
-    sdk.call("tensor_fill_normal", t["x_silu"], 1, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["x_gelu"], 1, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["a"], 1, 1, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["b"], 1, 2, 0.0, 1.0)
-    sdk.synchronize()
+    # Each kernel gets its own rotation of identical operand sets, at least
+    # 600 MB apart in traffic, so no launch finds its operands in the 256 MB
+    # last-level cache.
+    def filled(dtype, shape, stream_id):
+        x = sdk.tensor(dtype, shape)
+        sdk.call("tensor_fill_normal", x, 1, stream_id, 0.0, 1.0)
+        return x
 
-    ops = cfg2_ops(sdk, t)
-    for _ in range(args.warmup):
-        for _, fn in ops:
-            fn()
+    def unary_sets():
+        return [(filled("f16", (8192, 8192), 0), sdk.tensor("f16", (8192, 8192)))
+                for _ in range(3)]
+
+    silu_sets, gelu_sets = unary_sets(), unary_sets()
+    swiglu_sets = [(filled("f16", (4096, 16384), 1), filled("f16", (4096, 16384), 2),
+                    sdk.tensor("f16", (4096, 16384))) for _ in range(2)]
     sdk.synchronize()
-    timer = Timer(hip, stream)
+    phases = [
+        ("silu_f16", lambda i: sdk.call("tensor_silu_f16", *silu_sets[i % 3])),
+        ("gelu_f16", lambda i: sdk.call("tensor_gelu_f16", *gelu_sets[i % 3])),
+        # out = a * silu(b): b is the SiLU'd (gate) operand, a the up operand
+        ("swiglu_f16", lambda i: sdk.call("tensor_silu_multiply_f16", swiglu_sets[i % 2][1],
+                                          swiglu_sets[i % 2][0], swiglu_sets[i % 2][2])),
+    ]
+    for i in range(args.warmup):
+        for _, fn in phases:
+            fn(i)
+    sdk.synchronize()
+    # Timed region: K launches of each kernel, back to back on the SDK
+    # stream, with one event before the first launch and one after each
+    # kernel's K launches: per-kernel average = its phase / K.
+    marks = [hip.event() for _ in range(len(phases) + 1)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        timer.chain(ops)
+    hip.record(marks[0], stream)
+    for j, (_, fn) in enumerate(phases):
+        for i in range(args.steps):
+            fn(i)
+        hip.record(marks[j + 1], stream)
     sdk.synchronize()
     wall = time.perf_counter() - t0
-    per_kernel = {name: sum(d) / len(d) for name, d in timer.durations().items()}
+    per_kernel = {name: hip.elapsed_ms(marks[j], marks[j + 1]) / args.steps
+                  for j, (name, _) in enumerate(phases)}
 
     step_bytes = sum(v[0] for v in CFG2.values())
     step_elems = sum(v[1] for v in CFG2.values())
@@ -363,8 +368,10 @@ def main():
                       "pct_peak": round(100 * CFG2[name][0] / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
                       "elements_per_s": float(f"{CFG2[name][1] / (ms * 1e-3):.4g}")}
                for name, ms in per_kernel.items()}
-    for v in t.values():
-        v.free()
+    for group in (silu_sets, gelu_sets, swiglu_sets):
+        for tensors in group:
+            for v in tensors:
+                v.free()
 
     line = {
         "metric": "achieved HBM GB/s and % of MI355X peak per tensor_ops kernel; elements/sec",
@@ -379,7 +386,8 @@ def main():
         "elements_per_s": float(f"{step_elems / (ms_per_step * 1e-3):.4g}"),
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                      "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic(dominant),
+                     "algorithmic_bytes": CFG2[dominant][0]},
         "kernels": kernels,
     }
     if not args.no_suite:
