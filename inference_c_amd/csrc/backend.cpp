@@ -143,8 +143,9 @@ int host_rope(T *q, T *k, size_t seq, size_t qh, size_t kh, size_t dim, double t
     void *pq = st.inout(q, qn * sizeof(T));
     void *pk = st.inout(k, kn * sizeof(T));
     if (st.failed()) return 0;
-    ScratchBlock table(k::rope_table_bytes(seq, dim));
-    if (table.get() == nullptr) return 0;
+    const size_t table_bytes = k::rope_table_bytes(seq, qh, kh, dim, sizeof(T), pq, pk);
+    ScratchBlock table(table_bytes);
+    if (table_bytes != 0 && table.get() == nullptr) return 0;
     hipError_t status;
     if constexpr (sizeof(T) == 4)
         status = k::rope_f32(static_cast<float *>(pq), static_cast<float *>(pk), seq, qh, kh, dim,

@@ -15,8 +15,9 @@
 //                         0.5 x (1 + tanh(u)) evaluated as x / (1 + e^(-2u)),
 //                         the same function without the cancellation of
 //                         1 + tanh(u) for u << 0, u = 0.7978845608 (x + 0.044715 x^3);
-//                         f16 outputs form u in f32 in the reference's operation
-//                         order, f32 outputs form it in double.
+//                         f16 outputs form the exponent as one f32 polynomial
+//                         and use v_exp_f32 / v_rcp_f32, f32 outputs form u in
+//                         double.
 #include "kern_common.hpp"
 #include "kernels.hpp"
 
@@ -24,10 +25,6 @@ namespace icsdk {
 namespace {
 
 // ---- op functors ---------------------------------------------------------
-
-__device__ inline float gelu_inner(float v) {
-    return 0.7978845608f * (v + 0.044715f * v * v * v);
-}
 
 // f32-output path: u in double, then e^(-2u) from a hi/lo split of -2u
 // (e^(hi+lo) = e^hi * (1 + lo) to f32 accuracy), so the result is a few f32
@@ -43,16 +40,28 @@ __device__ inline float gelu_sigmoid_precise(float v) {
     return v / (1.0f + e);
 }
 
+// f16-output path: the exponent -2u log2(e) as one polynomial,
+// t = v (c1 + c2 v^2) with c1 = -2 log2(e) 0.7978845608 and c2 = 0.044715 c1,
+// three VALU ops instead of seven (the kernel is VALU-bound at this op
+// count). t is within a few f32 ulps of the reference's exponent, so the
+// result moves by < 1e-5 relative, far inside half an f16 ulp (2.4e-4). The
+// x >= 5 clamp is implied here: there exp2(t) < 2^-24, 1 + exp2(t) rounds to
+// 1 and the result is x exactly (also for +inf); the x <= -5 clamp stays,
+// for the f16 subnormal results it forces to zero and for -inf.
+constexpr float kGeluC1 = (float)(-2.0 * 1.4426950408889634 * (double)0.7978845608f);
+constexpr float kGeluC2 = (float)((double)kGeluC1 * (double)0.044715f);
+
 template <bool kFast>
 __device__ inline float gelu(float v) {
-    float r;
     if constexpr (kFast) {
-        r = v * fast_rcp(1.0f + fast_exp(-2.0f * gelu_inner(v)));
+        const float t = v * __builtin_fmaf(kGeluC2, v * v, kGeluC1);
+        const float r = v * fast_rcp(1.0f + __builtin_amdgcn_exp2f(t));
+        return v <= -5.0f ? 0.0f : r;
     } else {
-        r = gelu_sigmoid_precise(v);
+        float r = gelu_sigmoid_precise(v);
+        r = v >= 5.0f ? v : r;
+        return v <= -5.0f ? 0.0f : r;
     }
-    r = v >= 5.0f ? v : r;
-    return v <= -5.0f ? 0.0f : r;
 }
 
 template <bool kFast>

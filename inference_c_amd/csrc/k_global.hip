@@ -1,21 +1,29 @@
 // Whole-tensor reductions for gfx950: sum+max of an f32 tensor and argmax.
 //
-// Two passes. Pass 1: a fixed grid (kPartials blocks) streams the tensor with
-// 16-byte loads, kUnroll vectors in flight per lane; each lane folds every
-// group of 16 values in f32 and adds the group total to an f64 accumulator,
-// so the rounding error stays near 16 f32 ulps of the group magnitude
-// regardless of the tensor size. Lanes combine through DPP/shuffles, waves
-// through LDS, and each block writes one partial. Pass 2: one block folds the
-// partials in f64 and writes the result. No atomics and no counters, so the
-// partial buffer needs no clearing between calls.
+// Two passes. Pass 1 (sum+max): block b streams the contiguous chunk of
+// kChunk 16-byte vectors starting at b * kChunk, kVpl vectors in flight per
+// lane per step (one-shot chunks measured ~15% faster on MI355X than a
+// persistent grid-stride loop: 88% vs 76% of HBM peak reading 4 GiB); past
+// kMaxPartials chunks the grid strides over chunks. Each lane folds every
+// step's 32 values in f32 and adds the step total to an f64 accumulator, so
+// the rounding error stays near 32 f32 ulps of the step magnitude regardless
+// of the tensor size. Lanes combine through shuffles, waves through LDS, and
+// each block writes one partial. Pass 2: one 1024-lane block loads all
+// partials at once, folds them in f64 and writes the result. No atomics and
+// no counters, so the partial buffer needs no clearing between calls.
 #include "kern_common.hpp"
 #include "kernels.hpp"
 
 namespace icsdk {
 namespace {
 
-constexpr int kPartials = 2048;
-constexpr int kUnroll = 4;
+constexpr int kPartials = 2048;     // argmax pass-1 grid
+constexpr int kUnroll = 4;          // argmax vectors in flight per lane
+constexpr int kVpl = 8;             // sum+max vectors in flight per lane
+constexpr int kSteps = 16;          // sum+max steps per chunk
+constexpr size_t kChunk = (size_t)kBlock * kVpl * kSteps;  // 512 KiB of f32
+constexpr int kMaxPartials = 8192;  // sum+max pass-1 grid cap (4 GiB per sweep)
+constexpr int kFoldBlock = 1024;    // pass-2 lanes
 
 struct Partial {
     double sum;
@@ -32,6 +40,36 @@ __device__ inline void fold(const f32x4 &v, float &group, float &m, bool &nan) {
     nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
 }
 
+// One chunk: kSteps steps of kVpl coalesced vectors per lane. kGuard: the
+// chunk runs past nvec (the last one), so vectors past the end are skipped.
+template <bool kGuard>
+__device__ inline void sum_max_chunk(const f32x4 *__restrict__ xv, size_t first, size_t nvec,
+                                     double &total, float &m, bool &nan) {
+#pragma unroll 1
+    for (int step = 0; step < kSteps; ++step) {
+        const size_t base = first + (size_t)step * kVpl * kBlock + threadIdx.x;
+        f32x4 v[kVpl];
+#pragma unroll
+        for (int u = 0; u < kVpl; ++u) {
+            const size_t i = base + (size_t)u * kBlock;
+            if constexpr (kGuard) {
+                v[u] = __builtin_nontemporal_load(xv + (i < nvec ? i : 0));
+            } else {
+                v[u] = __builtin_nontemporal_load(xv + i);
+            }
+        }
+        float group = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kVpl; ++u) {
+            if constexpr (kGuard) {
+                if (base + (size_t)u * kBlock >= nvec) continue;
+            }
+            fold(v[u], group, m, nan);
+        }
+        total += (double)group;
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void sum_max_pass1(const float *__restrict__ x,
                                                         size_t nvec, size_t n,
                                                         Partial *__restrict__ partials) {
@@ -39,25 +77,13 @@ __global__ __launch_bounds__(kBlock) void sum_max_pass1(const float *__restrict_
     __shared__ float lds_max[kBlock / kWave];
     __shared__ int lds_nan[kBlock / kWave];
     const f32x4 *xv = reinterpret_cast<const f32x4 *>(x);
-    const size_t stride = (size_t)gridDim.x * kBlock;
-    size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
     double total = 0.0;
     float m = -__builtin_inff();
     bool nan = false;
-    for (; i + (kUnroll - 1) * stride < nvec; i += kUnroll * stride) {
-        f32x4 v[kUnroll];
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(xv + i + u * stride);
-        float group = 0.0f;
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) fold(v[u], group, m, nan);
-        total += (double)group;
-    }
-    for (; i < nvec; i += stride) {
-        const f32x4 v = __builtin_nontemporal_load(xv + i);
-        float group = 0.0f;
-        fold(v, group, m, nan);
-        total += (double)group;
+    for (size_t chunk = blockIdx.x; chunk * kChunk < nvec; chunk += gridDim.x) {
+        const size_t first = chunk * kChunk;
+        if (first + kChunk <= nvec) sum_max_chunk<false>(xv, first, nvec, total, m, nan);
+        else sum_max_chunk<true>(xv, first, nvec, total, m, nan);
     }
     if (blockIdx.x == 0 && threadIdx.x < n - nvec * 4) {
         const float v = x[nvec * 4 + threadIdx.x];
@@ -88,19 +114,30 @@ __global__ __launch_bounds__(kBlock) void sum_max_pass1(const float *__restrict_
     }
 }
 
-__global__ __launch_bounds__(kBlock) void sum_max_pass2(const Partial *__restrict__ partials,
-                                                        int count, double *sum_out,
-                                                        float *max_out) {
-    __shared__ double lds_sum[kBlock / kWave];
-    __shared__ float lds_max[kBlock / kWave];
-    __shared__ int lds_nan[kBlock / kWave];
+// count <= kMaxPartials = 8 * kFoldBlock: every lane's partials are
+// requested before any is folded.
+__global__ __launch_bounds__(kFoldBlock) void sum_max_pass2(const Partial *__restrict__ partials,
+                                                            int count, double *sum_out,
+                                                            float *max_out) {
+    constexpr int kPer = kMaxPartials / kFoldBlock;
+    __shared__ double lds_sum[kFoldBlock / kWave];
+    __shared__ float lds_max[kFoldBlock / kWave];
+    __shared__ int lds_nan[kFoldBlock / kWave];
+    Partial p[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = (int)threadIdx.x + j * kFoldBlock;
+        p[j] = partials[i < count ? i : 0];
+    }
     double s = 0.0;
     float m = -__builtin_inff();
     bool nan = false;
-    for (int i = threadIdx.x; i < count; i += kBlock) {
-        s += partials[i].sum;
-        m = fmaxf(m, partials[i].max);
-        nan |= partials[i].max != partials[i].max;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        if ((int)threadIdx.x + j * kFoldBlock >= count) continue;
+        s += p[j].sum;
+        m = fmaxf(m, p[j].max);
+        nan |= p[j].max != p[j].max;
     }
     s = wave_sum_f64(s);
     m = wave_max(m);
@@ -116,7 +153,7 @@ __global__ __launch_bounds__(kBlock) void sum_max_pass2(const Partial *__restric
         double total = 0.0;
         float bm = -__builtin_inff();
         int any_nan = 0;
-        for (int w = 0; w < kBlock / kWave; ++w) {
+        for (int w = 0; w < kFoldBlock / kWave; ++w) {
             total += lds_sum[w];
             bm = fmaxf(bm, lds_max[w]);
             any_nan |= lds_nan[w];
@@ -218,17 +255,22 @@ inline int pass1_grid(size_t work) {
 
 namespace k {
 
-size_t grid_reduce_scratch_bytes() { return sizeof(Partial) * kPartials; }
+size_t grid_reduce_scratch_bytes() {
+    return sizeof(Partial) * (kMaxPartials > kPartials ? kMaxPartials : kPartials);
+}
 
 hipError_t sum_max_f32(const float *x, size_t n, double *sum_out, float *max_out,
                        void *partials, hipStream_t s) {
     if (n == 0) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15u) != 0) return hipErrorInvalidValue;
     const size_t nvec = n / 4;
-    const int grid = pass1_grid(nvec);
+    size_t chunks = (nvec + kChunk - 1) / kChunk;
+    if (chunks < 1) chunks = 1;
+    const int grid = chunks > (size_t)kMaxPartials ? kMaxPartials : (int)chunks;
     auto *p = static_cast<Partial *>(partials);
     hipLaunchKernelGGL(sum_max_pass1, dim3(grid), dim3(kBlock), 0, s, x, nvec, n, p);
-    hipLaunchKernelGGL(sum_max_pass2, dim3(1), dim3(kBlock), 0, s, p, grid, sum_out, max_out);
+    hipLaunchKernelGGL(sum_max_pass2, dim3(1), dim3(kFoldBlock), 0, s, p, grid, sum_out,
+                       max_out);
     return hipGetLastError();
 }
 

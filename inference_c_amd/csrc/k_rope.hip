@@ -1,20 +1,25 @@
 // Split-half (NeoX) rotary position embedding for gfx950, in place on
 // q [seq, q_heads, dim] and k [seq, k_heads, dim].
 //
-// Two kernels on the SDK stream:
-//   1. table: one lane per (position, pair d < dim/2) computes the rotation
-//      exactly as the reference does -- angle = (float)((double)(offset + p) /
-//      pow(theta, 2d/dim)) in double, then cosf/sinf in f32 -- into a
-//      (cos, sin) table of seq * dim/2 float pairs (1 MiB for 4096 x 32);
-//   2. rotate: one lane per 16-byte vector of q then k (rows of dim elements
-//      read and written contiguously, non-temporal hint); each lane also
-//      reads the vector holding the other half of its pairs (same cache
-//      lines) and the pairs' cos/sin from the table (L2-resident), and
-//      rotates in f32 (left*c - right*s, right*c + left*s, no contraction).
-//      A pure streaming pass over q and k.
-// The table lives in device scratch supplied by the caller.
+// Fused path (half = dim/2 a multiple of the 16-byte vector, half <= 128,
+// 16-byte aligned tensors): one kernel. The host computes the pair
+// denominators pow(theta, 2d/dim) in double with the C library's pow, as the
+// reference does, and passes them as kernel arguments. A block covers whole
+// positions: each lane first issues the loads of its (head row, chunk)
+// items -- the left vector (pairs d..d+E-1) and the right vector (pairs
+// d+half..) of the row, both streamed -- then a few lanes compute the
+// block's rotations, angle = (float)((double)(offset + p) / denom[d]) and
+// sincosf, into LDS, and after one barrier every lane rotates its pairs in
+// f32 (left*c - right*s, right*c + left*s, no contraction) and stores both
+// vectors. Every q/k byte is read once and written once; the angles cost
+// `half` sincos per position, shared by all heads of the position.
+//
+// Table path (other shapes): a table kernel computes the same (cos, sin) per
+// (position, pair) into device scratch, then one lane per pair rotates.
 #include "kern_common.hpp"
 #include "kernels.hpp"
+
+#include <cmath>
 
 namespace icsdk {
 namespace {
@@ -56,54 +61,7 @@ __device__ inline void rotate_pair(float l, float r, float c, float s, S &lo, S 
     ro = Elem<S>::store(r * c + l * s);
 }
 
-// One 16-byte vector per lane over the rows of q then the rows of k (each
-// row = one head at one position, dim elements): a wave reads and writes
-// whole rows contiguously. The vector holding the left chunk c of a pair
-// block and the one holding the right chunk c are `half / E` vectors apart (a
-// power of two, so the partner is index ^ (half/E)); each lane also loads its
-// partner's vector (same cache lines, so no extra HBM traffic) and writes its
-// own half of the rotation.
-template <typename S, int kPartnerXor>
-__global__ __launch_bounds__(kBlock) void rope_vec_kernel(S *__restrict__ q, S *__restrict__ k,
-                                                          const float2 *__restrict__ table,
-                                                          uint64_t q_vectors, uint64_t vectors,
-                                                          FastDiv q_heads, FastDiv k_heads,
-                                                          uint32_t dim) {
-    constexpr int E = Vec16<S>::N;
-    constexpr int kRowShift = __builtin_ctz(2 * kPartnerXor);  // vectors per head row = 2 * half/E
-    const uint64_t v = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    const bool active = v < vectors;
-    const bool in_q = v < q_vectors;
-    const uint64_t local = in_q ? v : v - q_vectors;   // vector index inside q or k
-    S *data = in_q ? q : k;
-    const uint64_t row = local >> kRowShift;
-    const uint32_t j = (uint32_t)(local & (2 * kPartnerXor - 1));
-    const uint32_t p = fast_div((uint32_t)row, in_q ? q_heads : k_heads);
-    const uint32_t half = dim / 2;
-    const bool left = j < (uint32_t)kPartnerXor;
-    const uint32_t d0 = (left ? j : j - kPartnerXor) * E;   // first pair of this vector
-    if (!active) return;
-    // the lane's own vector, its partner's vector (same head row, so the same
-    // cache lines) and its pairs' cos/sin (L1/L2-resident) are all requested
-    // before any is used
-    const Vec16<S> mine = load16_stream(data + local * E);
-    const Vec16<S> partner = load16(data + (local ^ (uint64_t)kPartnerXor) * E);
-    float2 cs[E];
-    const float2 *tp = table + (size_t)p * half + d0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) cs[e] = tp[e];
-    Vec16<S> out;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const float2 t = cs[e];
-        const float a = Elem<S>::load(mine.v[e]), b = Elem<S>::load(partner.v[e]);
-        // left lane: l*c - r*s with l = a, r = b; right lane: r*c + l*s with r = a, l = b
-        out.v[e] = Elem<S>::store(left ? a * t.x - b * t.y : a * t.x + b * t.y);
-    }
-    store16_stream(data + local * E, out);
-}
-
-// one pair per lane (head_dim/2 not a multiple of the vector, or unaligned)
+// table path: one pair per lane
 template <typename S>
 __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(S *__restrict__ q, S *__restrict__ k,
                                                              const float2 *__restrict__ table,
@@ -123,6 +81,111 @@ __global__ __launch_bounds__(kBlock) void rope_scalar_kernel(S *__restrict__ q, 
     }
 }
 
+
+// ---- fused path ------------------------------------------------------------
+
+constexpr int kMaxHalf = 128;       // pairs per head row on the fused path (<= kBlock)
+constexpr int kLdsPairs = 2048;     // (position, pair) rotations per block
+
+struct RopeDenoms {
+    double d[kMaxHalf];
+};
+
+// Item = (position, row, chunk): row < qh is a q head, else a k head; chunk
+// c covers pairs c*E .. c*E+E-1. Items are numbered position-major; block
+// (x, y) owns items y*kIt*kBlock .. +kIt*kBlock of positions x*ppb ..
+// x*ppb+ppb-1 and computes those positions' rotations. A lane handles kIt
+// items; its loads are issued unconditionally (a lane past the end re-reads
+// item 0, which lane 0 loads anyway) so that no branch makes it wait for one
+// item before requesting the next, and there is no loop, so nothing waits
+// for the loads before the rotations are computed.
+template <typename S, int kChunks, int kIt>
+__global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S *__restrict__ k,
+                                                            uint32_t seq, uint32_t qh,
+                                                            uint32_t kh, uint32_t ppb,
+                                                            uint64_t offset, RopeDenoms denom) {
+    constexpr int E = Vec16<S>::N;
+    constexpr uint32_t half = kChunks * E;
+    extern __shared__ float2 rot[];  // ppb * half rotations
+    const uint32_t heads = qh + kh;
+    const uint32_t per_pos = heads * kChunks;
+    const uint32_t p0 = blockIdx.x * ppb;
+    const uint32_t npos = min(ppb, seq - p0);
+    const uint32_t items = npos * per_pos;
+    const uint32_t rot_entries = npos * half;
+    const uint32_t it0 = blockIdx.y * (uint32_t)(kIt * kBlock);
+    Vec16<S> lv[kIt], rv[kIt];
+    S *row_ptr[kIt];
+    uint32_t slot[kIt];  // index of the item's first rotation in `rot`
+    bool ok[kIt];
+#pragma unroll
+    for (int u = 0; u < kIt; ++u) {
+        const uint32_t raw = it0 + threadIdx.x + u * kBlock;
+        ok[u] = raw < items;
+        const uint32_t item = ok[u] ? raw : 0u;
+        const uint32_t pp = item / per_pos;
+        const uint32_t rest = item - pp * per_pos;
+        const uint32_t row = rest / kChunks;
+        const uint32_t c = rest - row * kChunks;
+        const size_t p = (size_t)p0 + pp;
+        S *base = row < qh ? q + (p * qh + row) * (2 * half)
+                           : k + (p * kh + (row - qh)) * (2 * half);
+        row_ptr[u] = base + c * E;
+        slot[u] = pp * half + c * E;
+        lv[u] = load16_stream(row_ptr[u]);
+        rv[u] = load16_stream(row_ptr[u] + half);
+    }
+    // The denominators go to LDS through scalar loads (uniform addresses,
+    // counted by lgkmcnt), so computing the rotations never waits for the
+    // data loads above, which are counted by vmcnt.
+    __shared__ double den[half];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (uint32_t d = 0; d < half; ++d) den[d] = denom.d[d];
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < rot_entries; e += kBlock) {
+        const uint32_t pp = e / half;
+        const float angle = (float)((double)(offset + p0 + pp) / den[e & (half - 1)]);
+        float c, sn;
+        sincosf(angle, &sn, &c);
+        rot[e] = make_float2(c, sn);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kIt; ++u) {
+        if (!ok[u]) continue;
+        Vec16<S> lo, ro;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float2 t = rot[slot[u] + e];
+            const float l = Elem<S>::load(lv[u].v[e]), r = Elem<S>::load(rv[u].v[e]);
+            lo.v[e] = Elem<S>::store(l * t.x - r * t.y);
+            ro.v[e] = Elem<S>::store(r * t.x + l * t.y);
+        }
+        store16_stream(row_ptr[u], lo);
+        store16_stream(row_ptr[u] + half, ro);
+    }
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Vectors per half row on the fused path, or 0 when the shape takes the
+// table path.
+template <typename S>
+uint32_t fused_chunks(size_t seq, size_t qh, size_t kh, size_t dim, const void *q,
+                      const void *k) {
+    constexpr size_t E = Vec16<S>::N;
+    const size_t half = dim / 2;
+    if (half % E != 0 || half > (size_t)kMaxHalf || !aligned16(q) || !aligned16(k)) return 0;
+    const size_t chunks = half / E;
+    if (chunks != 1 && chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16 && chunks != 32)
+        return 0;
+    // grid.x * kBlock work-items must stay below 2^32; grid.y <= 16384
+    if (seq > (size_t{1} << 24) || (qh + kh) * chunks > 0xffffffu) return 0;
+    return (uint32_t)chunks;
+}
+
 template <typename S>
 hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim, double theta,
                        size_t offset, void *table_scratch, hipStream_t s) {
@@ -130,39 +193,59 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
     const size_t half = dim / 2;
     if (dim == 0 || dim % 2 || seq * half > 0xffffffffu || qh + kh > 0xffffffu)
         return hipErrorInvalidValue;
+    const size_t heads = qh + kh;
+    if (const uint32_t chunks = fused_chunks<S>(seq, qh, kh, dim, q, k)) {
+        RopeDenoms denom{};
+        for (size_t d = 0; d < half; ++d)
+            denom.d[d] = std::pow(theta, (2.0 * (double)d) / (double)dim);
+        // whole positions per block: about one item per lane, and at most
+        // kLdsPairs rotations
+        const size_t per_pos = heads * chunks;
+        size_t ppb = per_pos >= (size_t)kBlock ? 1 : (size_t)kBlock / per_pos;
+        if (ppb * half > (size_t)kLdsPairs) ppb = (size_t)kLdsPairs / half;
+        if (ppb < 1) ppb = 1;
+        const uint32_t a = (uint32_t)seq, b = (uint32_t)qh, c = (uint32_t)kh, d = (uint32_t)ppb;
+        // items per lane: 1, 2 or 4; positions with more items than 4 per
+        // lane are split over blockIdx.y
+        const size_t lanes_needed = (ppb * per_pos + kBlock - 1) / kBlock;
+        const int it = lanes_needed <= 1 ? 1 : lanes_needed <= 2 ? 2 : 4;
+        const size_t splits = (ppb * per_pos + (size_t)it * kBlock - 1) / ((size_t)it * kBlock);
+        const dim3 grid((unsigned)((seq + ppb - 1) / ppb), (unsigned)splits), block(kBlock);
+        const size_t lds = ppb * half * sizeof(float2);
+#define ICSDK_ROPE(CH, IT)                                                                      \
+    hipLaunchKernelGGL((rope_fused_kernel<S, CH, IT>), grid, block, lds, s, q, k, a, b, c, d,    \
+                       (uint64_t)offset, denom)
+#define ICSDK_ROPE_IT(CH)                                                                       \
+    do {                                                                                        \
+        if (it == 1) ICSDK_ROPE(CH, 1);                                                         \
+        else if (it == 2) ICSDK_ROPE(CH, 2);                                                    \
+        else ICSDK_ROPE(CH, 4);                                                                 \
+    } while (0)
+        switch (chunks) {
+            case 1: ICSDK_ROPE_IT(1); break;
+            case 2: ICSDK_ROPE_IT(2); break;
+            case 4: ICSDK_ROPE_IT(4); break;
+            case 8: ICSDK_ROPE_IT(8); break;
+            case 16: ICSDK_ROPE_IT(16); break;
+            default: ICSDK_ROPE_IT(32); break;
+        }
+#undef ICSDK_ROPE_IT
+#undef ICSDK_ROPE
+        return hipGetLastError();
+    }
+    if (table_scratch == nullptr) return hipErrorInvalidValue;
     auto *table = static_cast<float2 *>(table_scratch);
     const size_t entries = seq * half;
     hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((entries + kBlock - 1) / kBlock)),
                        dim3(kBlock), 0, s, table, (uint32_t)seq, (uint32_t)half, (uint32_t)dim,
                        theta, (uint64_t)offset);
-    constexpr size_t E = Vec16<S>::N;
-    const size_t heads = qh + kh;
-    const size_t chunks = half / E;  // vectors per half row
-    const bool vector = half % E == 0 && chunks >= 1 && chunks <= 32 &&
-                        (chunks & (chunks - 1)) == 0 && ((uintptr_t)q & 15u) == 0 &&
-                        ((uintptr_t)k & 15u) == 0 && seq * heads < (size_t{1} << 32);
-    if (vector) {
-        const uint64_t q_vectors = (uint64_t)seq * qh * (dim / E);
-        const uint64_t vectors = q_vectors + (uint64_t)seq * kh * (dim / E);
-        const dim3 grid((unsigned)((vectors + kBlock - 1) / kBlock)), block(kBlock);
-        const FastDiv qd = make_fast_div((uint32_t)qh), kd = make_fast_div((uint32_t)kh);
-        switch (chunks) {
-            case 1: hipLaunchKernelGGL((rope_vec_kernel<S, 1>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-            case 2: hipLaunchKernelGGL((rope_vec_kernel<S, 2>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-            case 4: hipLaunchKernelGGL((rope_vec_kernel<S, 4>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-            case 8: hipLaunchKernelGGL((rope_vec_kernel<S, 8>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-            case 16: hipLaunchKernelGGL((rope_vec_kernel<S, 16>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-            default: hipLaunchKernelGGL((rope_vec_kernel<S, 32>), grid, block, 0, s, q, k, table, q_vectors, vectors, qd, kd, (uint32_t)dim); break;
-        }
-    } else {
-        const size_t per_pos = heads * half;
-        const size_t items = seq * per_pos;
-        size_t grid = (items + kBlock - 1) / kBlock;
-        if (grid > (size_t{1} << 20)) grid = size_t{1} << 20;
-        hipLaunchKernelGGL((rope_scalar_kernel<S>), dim3((unsigned)grid), dim3(kBlock), 0, s, q, k,
-                           table, items, per_pos, (uint32_t)half, (uint32_t)qh, (uint32_t)kh,
-                           (uint32_t)dim);
-    }
+    const size_t per_pos = heads * half;
+    const size_t items = seq * per_pos;
+    size_t grid = (items + kBlock - 1) / kBlock;
+    if (grid > (size_t{1} << 20)) grid = size_t{1} << 20;
+    hipLaunchKernelGGL((rope_scalar_kernel<S>), dim3((unsigned)grid), dim3(kBlock), 0, s, q, k,
+                       table, items, per_pos, (uint32_t)half, (uint32_t)qh, (uint32_t)kh,
+                       (uint32_t)dim);
     return hipGetLastError();
 }
 
@@ -170,7 +253,12 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
 
 namespace k {
 
-size_t rope_table_bytes(size_t seq, size_t dim) { return seq * (dim / 2) * sizeof(float2); }
+size_t rope_table_bytes(size_t seq, size_t qh, size_t kh, size_t dim, size_t elem,
+                        const void *q, const void *k) {
+    const bool fused = elem == 4 ? fused_chunks<float>(seq, qh, kh, dim, q, k) != 0
+                                 : fused_chunks<_Float16>(seq, qh, kh, dim, q, k) != 0;
+    return fused ? 0 : seq * (dim / 2) * sizeof(float2);
+}
 
 hipError_t rope_f32(float *q, float *k, size_t seq, size_t qh, size_t kh, size_t dim,
                     double theta, size_t offset, void *table, hipStream_t s) {

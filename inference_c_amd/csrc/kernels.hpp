@@ -69,10 +69,12 @@ hipError_t argmax_f32(const float *x, size_t n, uint32_t *index_out, void *parti
 hipError_t argmax_f16(const uint16_t *x, size_t n, uint32_t *index_out, void *partials,
                       hipStream_t s);
 
-// In-place split-half RoPE on q [seq, qh, dim] and k [seq, kh, dim]. `table`
-// is device scratch of rope_table_bytes(seq, dim) bytes (the per-call
-// cos/sin table).
-size_t rope_table_bytes(size_t seq, size_t dim);
+// In-place split-half RoPE on q [seq, qh, dim] and k [seq, kh, dim].
+// Shapes whose half row is a multiple of the 16-byte vector (<= 128 pairs,
+// aligned tensors) need no scratch; others need `table`, device scratch of
+// rope_table_bytes(...) bytes (the per-call cos/sin table). 0 = none needed.
+size_t rope_table_bytes(size_t seq, size_t qh, size_t kh, size_t dim, size_t elem,
+                        const void *q, const void *k);
 hipError_t rope_f32(float *q, float *k, size_t seq, size_t qh, size_t kh, size_t dim,
                     double theta, size_t offset, void *table, hipStream_t s);
 hipError_t rope_f16(uint16_t *q, uint16_t *k, size_t seq, size_t qh, size_t kh,

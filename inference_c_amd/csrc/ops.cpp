@@ -349,8 +349,10 @@ int rope(TensorDType dtype, TensorBuffer *q, TensorBuffer *k, size_t qh, size_t 
     void *pq = srcdst(st, q);
     void *pk = srcdst(st, k);
     if (st.failed()) return 0;
-    ScratchBlock table(k::rope_table_bytes(seq, dim));
-    if (table.get() == nullptr) {
+    const size_t table_bytes =
+        k::rope_table_bytes(seq, qh, kh, dim, dtype == TENSOR_DTYPE_F32 ? 4 : 2, pq, pk);
+    ScratchBlock table(table_bytes);
+    if (table_bytes != 0 && table.get() == nullptr) {
         set_error(error, capacity, "RoPE: out of device memory for the angle table");
         return 0;
     }
