@@ -82,7 +82,10 @@ struct RowSlot {
     uint32_t t;
     __device__ RowSlot() {
         if constexpr (WPR == 1) {
-            row = (size_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+            // the wave index is wave-uniform; readfirstlane tells the compiler,
+            // so the row and its base addresses live in scalar registers
+            row = (size_t)blockIdx.x * (kBlock / kWave) +
+                  (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
             t = threadIdx.x & (kWave - 1);
         } else {
             row = blockIdx.x;
@@ -91,13 +94,17 @@ struct RowSlot {
     }
 };
 
-template <typename S, int NV, int WPR>
+// kExact: the row is exactly NV * WPR * 64 vectors (checked on the host), so
+// no lane needs a bounds check.
+template <typename S, int NV, int WPR, bool kExact = false>
 struct RowRegs {
     static constexpr int E = Vec16<S>::N;
     static constexpr uint32_t T = WPR * kWave;
     float v[NV][E];
 
-    __device__ inline bool valid(int j, uint32_t t, uint32_t vpr) const { return t + j * T < vpr; }
+    __device__ static inline bool valid(int j, uint32_t t, uint32_t vpr) {
+        return kExact || t + j * T < vpr;
+    }
 
     // Every load is issued unconditionally (a lane past the row end re-reads
     // vector 0 of the row) and the fill value selected afterwards: a guarded
@@ -117,51 +124,58 @@ struct RowRegs {
 
     __device__ static inline uint32_t clamp(int j, uint32_t t, uint32_t vpr) {
         const uint32_t vi = t + j * T;
-        return vi < vpr ? vi : 0u;
+        return kExact || vi < vpr ? vi : 0u;
     }
 };
 
 // Unconditional loads of a per-column parameter slice (weights, scale, bias).
-template <typename S, int NV, int WPR>
+template <typename S, int NV, int WPR, bool kExact = false>
 __device__ inline void load_params(const S *p, uint32_t t, uint32_t vpr, Vec16<S> (&out)[NV]) {
-    using R = RowRegs<S, NV, WPR>;
+    using R = RowRegs<S, NV, WPR, kExact>;
 #pragma unroll
     for (int j = 0; j < NV; ++j) out[j] = load16(p + (size_t)R::clamp(j, t, vpr) * R::E);
 }
 
 // ---- RMSNorm / fused residual + RMSNorm ------------------------------------
 
-template <typename S, int NV, int WPR, bool kResidual>
+// The weight slice is requested first and pinned there (a scheduling
+// barrier): it comes from L2, and left to the scheduler its loads sink below
+// the row reduction, adding an L2 round trip to every row's critical path.
+// Outputs are written through L2 (OutWindow).
+template <typename S, int NV, int WPR, bool kResidual, bool kExact>
 __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
     const S *__restrict__ x, const S *__restrict__ residual, S *__restrict__ sum_out,
     const S *__restrict__ w, S *__restrict__ y, size_t rows, uint32_t width, float eps) {
     __shared__ float lds[kBlock / kWave];
-    using R = RowRegs<S, NV, WPR>;
+    using R = RowRegs<S, NV, WPR, kExact>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
     if (slot.row >= rows) return;
     const uint32_t vpr = width / E;
     const size_t base = slot.row * width;
+    Vec16<S> wv[NV];
+    load_params<S, NV, WPR, kExact>(w, slot.t, vpr, wv);
+    __builtin_amdgcn_sched_barrier(0);
     R r;
     r.load(x + base, slot.t, vpr, 0.0f);
-    // the weight slice is fetched (from L2) while the row is still in flight
-    Vec16<S> wv[NV];
-    load_params<S, NV, WPR>(w, slot.t, vpr, wv);
+    const uint32_t row_bytes = width * (uint32_t)sizeof(S);
     if constexpr (kResidual) {
         Vec16<S> rv[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             rv[j] = load16_stream(residual + base + (size_t)R::clamp(j, slot.t, vpr) * E);
+        const OutWindow sums(sum_out + base, row_bytes);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const uint32_t vi = slot.t + j * R::T;
+            const bool ok = R::valid(j, slot.t, vpr);
             Vec16<S> sum;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 sum.v[e] = Elem<S>::store(r.v[j][e] + Elem<S>::load(rv[j].v[e]));
-                r.v[j][e] = vi < vpr ? Elem<S>::load(sum.v[e]) : 0.0f;
+                r.v[j][e] = ok ? Elem<S>::load(sum.v[e]) : 0.0f;
             }
-            if (vi < vpr) store16_stream(sum_out + base + (size_t)vi * E, sum);
+            if (ok) sums.store16(vi * 16u, sum);
         }
     }
     float squares = 0.0f;
@@ -171,15 +185,16 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
         for (int e = 0; e < E; ++e) squares += r.v[j][e] * r.v[j][e];
     squares = group_sum<WPR>(squares, lds);
     const float scale = 1.0f / sqrtf(squares / (float)width + eps);
+    const OutWindow out(y + base, row_bytes);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
-        if (vi < vpr) {
-            Vec16<S> out;
+        if (R::valid(j, slot.t, vpr)) {
+            Vec16<S> o;
 #pragma unroll
             for (int e = 0; e < E; ++e)
-                out.v[e] = Elem<S>::store(r.v[j][e] * scale * Elem<S>::load(wv[j].v[e]));
-            store16_stream(y + base + (size_t)vi * E, out);
+                o.v[e] = Elem<S>::store(r.v[j][e] * scale * Elem<S>::load(wv[j].v[e]));
+            out.store16(vi * 16u, o);
         }
     }
 }
@@ -555,10 +570,18 @@ hipError_t launch_rms(const S *x, const S *residual, S *sum_out, const S *w, S *
     const bool aligned = aligned16(x) && aligned16(residual) && aligned16(sum_out) &&
                          aligned16(w) && aligned16(y);
     if (pick_row_shape(width, sizeof(S), aligned, &shape)) {
+        const bool exact = width / (16 / sizeof(S)) == (size_t)shape.nv * shape.wpr * kWave;
 #define ICSDK_RMS(NV, WPR)                                                                 \
-    hipLaunchKernelGGL((rms_norm_kernel<S, NV, WPR, kResidual>), row_grid(rows, WPR),       \
-                       dim3(kBlock), 0, s, x, residual, sum_out, w, y, rows,              \
-                       (uint32_t)width, eps)
+    do {                                                                                   \
+        if (exact)                                                                         \
+            hipLaunchKernelGGL((rms_norm_kernel<S, NV, WPR, kResidual, true>),             \
+                               row_grid(rows, WPR), dim3(kBlock), 0, s, x, residual,       \
+                               sum_out, w, y, rows, (uint32_t)width, eps);                 \
+        else                                                                               \
+            hipLaunchKernelGGL((rms_norm_kernel<S, NV, WPR, kResidual, false>),            \
+                               row_grid(rows, WPR), dim3(kBlock), 0, s, x, residual,       \
+                               sum_out, w, y, rows, (uint32_t)width, eps);                 \
+    } while (0)
         ICSDK_ROW_DISPATCH(shape, ICSDK_RMS);
 #undef ICSDK_RMS
     } else {

@@ -2,94 +2,172 @@
 //     y[i] = (x[view(i)] + addend[bcast(i)]) * mult[bcast(i)]
 // with y contiguous in the view's shape.
 //
-// Four paths, chosen on the host from the strides:
-//   vector  - the view's last dimension is contiguous in x (stride 1) and all
-//             offsets are multiples of the 16-byte vector: every lane
-//             decomposes its output-vector index with multiply-high
-//             divisions, gathers one 16-byte vector of x (each a run of the
-//             innermost dimension), applies the broadcast operands (a vector
-//             when the operand spans the last dimension, a scalar when it is
-//             broadcast along it) and stores 16 bytes;
-//   vector tile - as vector, but the output dim next to the last one is not
-//             adjacent to it in x while another dim is (a permutation such as
-//             (0,2,1,3)): 8x8 tiles of contiguous runs are transposed through
-//             LDS so that reads and writes are both contiguous 8-run rows;
+// The host first coalesces the view: dimensions of extent 1 are dropped and a
+// dimension is merged into its inner neighbour when x, the addend and the
+// multiplier all step through both as through one (a contiguous tensor
+// becomes rank 1, a (0,2,1,3) permutation stays rank 4). Then one of three
+// paths runs, chosen from the coalesced strides:
+//   gather  - the innermost dimension is contiguous in x and every offset is
+//             a multiple of the 16-byte vector. One output vector per lane on
+//             a one-shot grid: the block's outer coordinates are decomposed
+//             once per block, the lane adds its (row, vector) offsets, loads
+//             one 16-byte run of x, applies the broadcast operands (a vector
+//             where the operand varies along the innermost dimension, a
+//             scalar where it is broadcast along it) and stores 16 bytes
+//             through L2. Each run is a whole contiguous vector, so no loaded
+//             byte is wasted and no staging is needed; measured on MI355X
+//             this beats staging the same permutation through LDS tiles at
+//             every run length from 16 to 256 bytes;
 //   tile    - x's contiguous dimension is another view dimension p (a
-//             transpose of p with the last dimension): 64x64 tiles are read
-//             along p, staged through LDS (padded against bank conflicts) and
-//             written along the last dimension, so both sides stay coalesced;
+//             transpose of p with the innermost dimension): 64x64 tiles are
+//             read along p, staged through LDS (padded against bank
+//             conflicts) and written along the innermost dimension, so both
+//             HBM streams stay coalesced;
 //   scalar  - anything else: one element per lane.
 #include "kern_common.hpp"
 #include "kernels.hpp"
+
+#include <algorithm>
 
 namespace icsdk {
 namespace {
 
 constexpr int kMaxRank = 8;
 
-struct ViewPlan {
+// The view after coalescing (element strides; 0 where an operand broadcasts).
+struct Coalesced {
     int rank;
-    FastDiv dims[kMaxRank];        // output extents (last one in vectors for the vector path)
-    int64_t x_stride[kMaxRank];    // x element strides
-    uint64_t a_stride[kMaxRank];   // addend element strides (0 where broadcast)
-    uint64_t m_stride[kMaxRank];   // multiplier element strides (0 where broadcast)
-    uint64_t x_offset;
-    int a_vec;                     // addend varies along the last dim
-    int m_vec;                     // multiplier varies along the last dim
+    uint64_t shape[kMaxRank];
+    int64_t x_stride[kMaxRank];
+    uint64_t a_stride[kMaxRank];
+    uint64_t m_stride[kMaxRank];
 };
 
-template <typename S>
-__device__ inline float opt_load(const S *p, uint64_t i) {
-    return Elem<S>::load(p[i]);
+// Contiguous strides of a broadcast operand, zeroed where its dim is 1.
+inline void broadcast_strides(const uint64_t *shape, int rank, uint64_t *out) {
+    uint64_t s = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+        out[d] = shape[d] == 1 ? 0 : s;
+        s *= shape[d];
+    }
 }
 
-// ---- vector path -------------------------------------------------------------
-
-template <typename S>
-__global__ __launch_bounds__(kBlock) void view_vec_kernel(const S *__restrict__ x,
-                                                          const S *__restrict__ addend,
-                                                          const S *__restrict__ mult,
-                                                          S *__restrict__ y, uint32_t nvec,
-                                                          ViewPlan plan) {
-    constexpr int E = Vec16<S>::N;
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        uint32_t rest = v;
-        int64_t xo = (int64_t)plan.x_offset;
-        uint64_t ao = 0, mo = 0;
-#pragma unroll
-        for (int d = kMaxRank - 1; d >= 0; --d) {
-            if (d < plan.rank) {
-                const uint32_t q = fast_div(rest, plan.dims[d]);
-                uint32_t idx = rest - q * plan.dims[d].divisor;
-                rest = q;
-                if (d == plan.rank - 1) idx *= E;  // last dim counted in vectors
-                xo += (int64_t)idx * plan.x_stride[d];
-                ao += (uint64_t)idx * plan.a_stride[d];
-                mo += (uint64_t)idx * plan.m_stride[d];
+Coalesced coalesce(const k::ViewArgs &v, const uint64_t *a_stride, const uint64_t *m_stride) {
+    Coalesced c{};
+    // walk from the innermost dimension outwards, building c back to front
+    int r = 0;
+    uint64_t shape[kMaxRank];
+    int64_t xs[kMaxRank];
+    uint64_t as[kMaxRank], ms[kMaxRank];
+    for (int d = v.rank - 1; d >= 0; --d) {
+        if (v.shape[d] == 1) continue;
+        if (r > 0) {
+            const int in = r - 1;
+            const bool merge = v.strides[d] == xs[in] * (int64_t)shape[in] &&
+                               a_stride[d] == as[in] * shape[in] &&
+                               m_stride[d] == ms[in] * shape[in];
+            if (merge) {
+                shape[in] *= v.shape[d];
+                continue;
             }
         }
-        const Vec16<S> xv = load16(x + xo);
-        Vec16<S> av{}, mv{};
-        float as = 0.0f, ms = 1.0f;
-        if (addend) {
-            if (plan.a_vec) av = load16(addend + ao);
-            else as = Elem<S>::load(addend[ao]);
-        }
-        if (mult) {
-            if (plan.m_vec) mv = load16(mult + mo);
-            else ms = Elem<S>::load(mult[mo]);
-        }
-        Vec16<S> out;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            float r = Elem<S>::load(xv.v[e]);
-            if (addend) r = r + (plan.a_vec ? Elem<S>::load(av.v[e]) : as);
-            if (mult) r = r * (plan.m_vec ? Elem<S>::load(mv.v[e]) : ms);
-            out.v[e] = Elem<S>::store(r);
-        }
-        store16_stream(y + (size_t)v * E, out);
+        shape[r] = v.shape[d];
+        xs[r] = v.strides[d];
+        as[r] = a_stride[d];
+        ms[r] = m_stride[d];
+        ++r;
     }
+    if (r == 0) {  // every extent is 1
+        shape[0] = 1;
+        xs[0] = 1;
+        as[0] = ms[0] = 0;
+        r = 1;
+    }
+    c.rank = r;
+    for (int i = 0; i < r; ++i) {
+        c.shape[i] = shape[r - 1 - i];
+        c.x_stride[i] = xs[r - 1 - i];
+        c.a_stride[i] = as[r - 1 - i];
+        c.m_stride[i] = ms[r - 1 - i];
+    }
+    return c;
+}
+
+// ---- gather path -------------------------------------------------------------
+
+// The coalesced view is split into outer dims 0..R-3 and an inner plane of
+// dims R-2 (rows) and R-1 (runs, counted in 16-byte vectors). A block covers
+// kBlock consecutive vectors of one inner plane: its outer coordinates and
+// their offsets are decomposed once per block from blockIdx (block-uniform,
+// so the compiler keeps them in scalar registers and off the vector ALU),
+// and each lane only splits its plane index into (row, vector) and adds two
+// products per operand, in 32 bits. The quarter-rate 32-bit multiplies of a
+// full per-lane decomposition otherwise sit between every lane and its load.
+struct GatherPlan {
+    int outer_rank;                // dims 0..outer_rank-1 (R - 2, or 0)
+    FastDiv outer[kMaxRank];       // their extents
+    uint64_t ox[kMaxRank], oa[kMaxRank], om[kMaxRank];  // their element strides
+    FastDiv plane_blocks;          // blocks per inner plane
+    FastDiv vecs;                  // vectors per row (innermost extent / E)
+    int vecs_log2;                 // log2(vecs) when vecs is a power of two, else -1
+    uint32_t plane;                // vectors per inner plane (rows * vecs)
+    uint32_t row_x, row_a, row_m;  // element strides of the row dim
+    uint64_t x_offset;
+};
+
+// How a broadcast operand enters: absent, one 16-byte vector per output
+// vector (it varies along the innermost dimension) or one element per output
+// vector (broadcast along it). A compile-time choice, so that every load of
+// the kernel is unconditional: a load behind a run-time branch is followed by
+// a wait for all outstanding loads, which would serialise the three streams.
+enum OperandKind { kNone = 0, kVector = 1, kScalar = 2 };
+
+template <typename S, int kA, int kM>
+__global__ __launch_bounds__(kBlock) void view_gather_kernel(const S *__restrict__ x,
+                                                             const S *__restrict__ addend,
+                                                             const S *__restrict__ mult,
+                                                             S *__restrict__ y,
+                                                             GatherPlan plan) {
+    constexpr int E = Vec16<S>::N;
+    // block-uniform part
+    const uint32_t b = blockIdx.x;
+    uint32_t outer = fast_div(b, plan.plane_blocks);
+    const uint32_t in_block = b - outer * plan.plane_blocks.divisor;
+    const uint64_t out_vec0 = (uint64_t)outer * plan.plane + (uint64_t)in_block * kBlock;
+    uint64_t xb = plan.x_offset, ab = 0, mb = 0;
+    for (int d = plan.outer_rank - 1; d >= 0; --d) {
+        uint32_t idx = outer;
+        if (d > 0) {
+            const uint32_t q = fast_div(outer, plan.outer[d]);
+            idx = outer - q * plan.outer[d].divisor;
+            outer = q;
+        }
+        xb += idx * plan.ox[d];
+        ab += idx * plan.oa[d];
+        mb += idx * plan.om[d];
+    }
+    // lane part
+    const uint32_t t = in_block * kBlock + threadIdx.x;  // vector index inside the plane
+    if (t >= plan.plane) return;
+    const uint32_t row = plan.vecs_log2 >= 0 ? t >> plan.vecs_log2 : fast_div(t, plan.vecs);
+    const uint32_t vec = t - row * plan.vecs.divisor;
+    const Vec16<S> xv = load16_stream(x + xb + (row * plan.row_x + vec * E));
+    Vec16<S> av, mv;
+    float a_scalar = 0.0f, m_scalar = 1.0f;
+    if constexpr (kA == kVector) av = load16(addend + ab + (row * plan.row_a + vec * E));
+    if constexpr (kA == kScalar) a_scalar = Elem<S>::load(addend[ab + row * plan.row_a]);
+    if constexpr (kM == kVector) mv = load16(mult + mb + (row * plan.row_m + vec * E));
+    if constexpr (kM == kScalar) m_scalar = Elem<S>::load(mult[mb + row * plan.row_m]);
+    Vec16<S> out;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        float r = Elem<S>::load(xv.v[e]);
+        if constexpr (kA != kNone) r = r + (kA == kVector ? Elem<S>::load(av.v[e]) : a_scalar);
+        if constexpr (kM != kNone) r = r * (kM == kVector ? Elem<S>::load(mv.v[e]) : m_scalar);
+        out.v[e] = Elem<S>::store(r);
+    }
+    const OutWindow window(y + out_vec0 * E, kBlock * 16u);
+    window.store16(threadIdx.x * 16u, out);
 }
 
 // ---- scalar path -------------------------------------------------------------
@@ -196,146 +274,60 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
     }
 }
 
-// ---- LDS-staged vector tile path ----------------------------------------------
-
-// For views whose last dimension L is contiguous in x and in the output but
-// whose next-outer output dimension o is not adjacent to L in x, while some
-// other dimension t is (x stride of t == L): e.g. a (0,2,1,3) permutation.
-// A block moves an 8 x 8 tile of (o, t) "units" (one unit = the L contiguous
-// elements, kVpu 16-byte vectors): it reads the tile as 8 rows of 8
-// x-contiguous units, stages them in LDS, and writes 8 rows of 8
-// output-contiguous units, so both HBM streams are contiguous runs of
-// 8 * L elements. LDS rows are padded by 128 bytes so that the 16-lane
-// phases of ds_read_b128 fall on disjoint banks when kVpu = 8.
-constexpr int kTileUnits = 8;
-
-struct TileVecPlan {
-    int rank;
-    int o, t;                       // tiled dims (o = rank - 2)
-    uint64_t shape[kMaxRank];
-    int64_t x_stride[kMaxRank];
-    uint64_t a_stride[kMaxRank];
-    uint64_t m_stride[kMaxRank];
-    uint64_t y_stride[kMaxRank];
-    uint64_t x_offset;
-    uint32_t tiles_o, tiles_t;
-    int a_vec, m_vec;
-};
-
-template <typename S, int kVpu>
-__global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(const S *__restrict__ x,
-                                                               const S *__restrict__ addend,
-                                                               const S *__restrict__ mult,
-                                                               S *__restrict__ y,
-                                                               TileVecPlan plan) {
-    constexpr int E = Vec16<S>::N;
-    constexpr int kRow = kTileUnits * kVpu + 8;  // vectors per LDS row (padded)
-    constexpr int kVecs = kTileUnits * kTileUnits * kVpu;
-    __shared__ Vec16<S> lds[kTileUnits * kRow];
-    const int last = plan.rank - 1;
-    const uint64_t block = blockIdx.x;
-    const uint32_t bt = (uint32_t)(block % plan.tiles_t);
-    const uint32_t bo = (uint32_t)((block / plan.tiles_t) % plan.tiles_o);
-    uint64_t batch = block / ((uint64_t)plan.tiles_t * plan.tiles_o);
-    int64_t xb = (int64_t)plan.x_offset;
-    uint64_t ab = 0, mb = 0, yb = 0;
-    for (int d = last - 1; d >= 0; --d) {
-        if (d == plan.o || d == plan.t) continue;
-        const uint64_t idx = batch % plan.shape[d];
-        batch /= plan.shape[d];
-        xb += (int64_t)idx * plan.x_stride[d];
-        ab += idx * plan.a_stride[d];
-        mb += idx * plan.m_stride[d];
-        yb += idx * plan.y_stride[d];
-    }
-    const uint64_t o0 = (uint64_t)bo * kTileUnits, t0 = (uint64_t)bt * kTileUnits;
-    const uint64_t no = plan.shape[plan.o], nt = plan.shape[plan.t];
-    constexpr int kPer = (kVecs + kBlock - 1) / kBlock;  // vectors per thread per phase
-    // read: o-rows of t-contiguous units (all of this thread's loads in flight)
-    Vec16<S> xin[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int v = threadIdx.x + u * kBlock;
-        const int oi = v / (kTileUnits * kVpu);
-        const int rem = v - oi * (kTileUnits * kVpu);
-        const int ti = rem / kVpu, c = rem - ti * kVpu;
-        const bool ok = v < kVecs && o0 + oi < no && t0 + ti < nt;
-        xin[u] = load16_stream(x + (ok ? xb + (int64_t)(o0 + oi) * plan.x_stride[plan.o] +
-                                              (int64_t)(t0 + ti) * plan.x_stride[plan.t] + c * E
-                                         : xb));
-    }
-    // the write phase's broadcast operands are fetched before the barrier
-    Vec16<S> av[kPer], mv[kPer];
-    float as[kPer], ms[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int v = threadIdx.x + u * kBlock;
-        const int ti = v / (kTileUnits * kVpu);
-        const int rem = v - ti * (kTileUnits * kVpu);
-        const int oi = rem / kVpu, c = rem - oi * kVpu;
-        const bool ok = v < kVecs && o0 + oi < no && t0 + ti < nt;
-        as[u] = 0.0f;
-        ms[u] = 1.0f;
-        if (addend) {
-            const uint64_t ao = ok ? ab + (t0 + ti) * plan.a_stride[plan.t] +
-                                         (o0 + oi) * plan.a_stride[plan.o] : 0;
-            if (plan.a_vec) av[u] = load16(addend + ao + (ok ? (uint64_t)c * E : 0));
-            else as[u] = Elem<S>::load(addend[ao]);
-        }
-        if (mult) {
-            const uint64_t mo = ok ? mb + (t0 + ti) * plan.m_stride[plan.t] +
-                                         (o0 + oi) * plan.m_stride[plan.o] : 0;
-            if (plan.m_vec) mv[u] = load16(mult + mo + (ok ? (uint64_t)c * E : 0));
-            else ms[u] = Elem<S>::load(mult[mo]);
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int v = threadIdx.x + u * kBlock;
-        const int oi = v / (kTileUnits * kVpu);
-        const int rem = v - oi * (kTileUnits * kVpu);
-        const int ti = rem / kVpu, c = rem - ti * kVpu;
-        if (v < kVecs) lds[oi * kRow + ti * kVpu + c] = xin[u];
-    }
-    __syncthreads();
-    // write: t-rows of o-contiguous units
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        const int v = threadIdx.x + u * kBlock;
-        const int ti = v / (kTileUnits * kVpu);
-        const int rem = v - ti * (kTileUnits * kVpu);
-        const int oi = rem / kVpu, c = rem - oi * kVpu;
-        if (v >= kVecs || o0 + oi >= no || t0 + ti >= nt) continue;
-        const Vec16<S> xv = lds[oi * kRow + ti * kVpu + c];
-        Vec16<S> out;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            float r = Elem<S>::load(xv.v[e]);
-            if (addend) r = r + (plan.a_vec ? Elem<S>::load(av[u].v[e]) : as[u]);
-            if (mult) r = r * (plan.m_vec ? Elem<S>::load(mv[u].v[e]) : ms[u]);
-            out.v[e] = Elem<S>::store(r);
-        }
-        store16_stream(y + yb + (t0 + ti) * plan.y_stride[plan.t] +
-                           (o0 + oi) * plan.y_stride[plan.o] + (uint64_t)c * E,
-                       out);
-    }
-}
-
 inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
-// Contiguous strides of a broadcast operand, zeroed where its dim is 1.
-inline void broadcast_strides(const uint64_t *shape, int rank, uint64_t *out) {
-    uint64_t s = 1;
-    for (int d = rank - 1; d >= 0; --d) {
-        out[d] = shape[d] == 1 ? 0 : s;
-        s *= shape[d];
+// Gather-path plan for a coalesced view, or false when the view does not fit
+// it: innermost dim not contiguous or not whole vectors, offsets not
+// vector-aligned, or a plane whose lane offsets or a grid that exceeds 32 bits.
+template <typename S>
+bool gather_plan(const Coalesced &c, uint64_t x_offset, uint64_t n, bool have_a, bool have_m,
+                 GatherPlan *plan, uint32_t *blocks) {
+    constexpr uint64_t E = Vec16<S>::N;
+    const int last = c.rank - 1;
+    if (c.x_stride[last] != 1 || c.shape[last] % E != 0 || x_offset % E != 0) return false;
+    const bool a_vec = have_a && c.a_stride[last] != 0;
+    const bool m_vec = have_m && c.m_stride[last] != 0;
+    for (int d = 0; d < last; ++d) {
+        if (c.x_stride[d] % E != 0) return false;
+        if (a_vec && c.a_stride[d] % E != 0) return false;
+        if (m_vec && c.m_stride[d] % E != 0) return false;
     }
+    const uint64_t vecs = c.shape[last] / E;
+    const uint64_t rows = c.rank >= 2 ? c.shape[last - 1] : 1;
+    const uint64_t row_x = c.rank >= 2 ? (uint64_t)c.x_stride[last - 1] : 0;
+    const uint64_t row_a = c.rank >= 2 ? c.a_stride[last - 1] : 0;
+    const uint64_t row_m = c.rank >= 2 ? c.m_stride[last - 1] : 0;
+    const uint64_t plane = rows * vecs;
+    const uint64_t plane_blocks = (plane + kBlock - 1) / kBlock;
+    const uint64_t outer = n / (plane * E);
+    const uint64_t lim = 0xffffffffull;
+    if (plane > lim / 2 || plane_blocks * outer > 0x7fffffffull || outer > lim ||
+        (rows - 1) * row_x + vecs * E > lim || (rows - 1) * row_a + vecs * E > lim ||
+        (rows - 1) * row_m + vecs * E > lim)
+        return false;
+    *plan = GatherPlan{};
+    plan->outer_rank = c.rank >= 2 ? c.rank - 2 : 0;
+    for (int d = 0; d < plan->outer_rank; ++d) {
+        plan->outer[d] = make_fast_div((uint32_t)c.shape[d]);
+        plan->ox[d] = (uint64_t)c.x_stride[d];
+        plan->oa[d] = c.a_stride[d];
+        plan->om[d] = c.m_stride[d];
+    }
+    plan->plane_blocks = make_fast_div((uint32_t)plane_blocks);
+    plan->vecs = make_fast_div((uint32_t)vecs);
+    plan->vecs_log2 = (vecs & (vecs - 1)) == 0 ? __builtin_ctzll(vecs) : -1;
+    plan->plane = (uint32_t)plane;
+    plan->row_x = (uint32_t)row_x;
+    plan->row_a = (uint32_t)row_a;
+    plan->row_m = (uint32_t)row_m;
+    plan->x_offset = x_offset;
+    *blocks = (uint32_t)(plane_blocks * outer);
+    return true;
 }
 
 template <typename S>
-hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend, const S *mult,
-                       S *y, hipStream_t s) {
-    constexpr int E = Vec16<S>::N;
+hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
+                       const S *mult, S *y, hipStream_t s) {
     const int rank = v.rank;
     if (rank < 1 || rank > kMaxRank) return hipErrorInvalidValue;
     uint64_t n = 1;
@@ -344,105 +336,56 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend, const 
     uint64_t a_stride[kMaxRank] = {}, m_stride[kMaxRank] = {};
     broadcast_strides(v.addend_shape, rank, a_stride);
     broadcast_strides(v.mult_shape, rank, m_stride);
-    const int last = rank - 1;
+    if (!addend) std::fill(a_stride, a_stride + rank, 0);
+    if (!mult) std::fill(m_stride, m_stride + rank, 0);
+    const Coalesced c = coalesce(v, a_stride, m_stride);
+    const int last = c.rank - 1;
 
-    // vector path
-    bool vec = v.strides[last] == 1 && v.shape[last] % E == 0 && v.offset % E == 0 &&
-               aligned16(x) && aligned16(y) && aligned16(addend) && aligned16(mult) &&
-               n / E < (uint64_t{1} << 32);
-    for (int d = 0; d < last && vec; ++d) vec = v.strides[d] % E == 0 && v.shape[d] < (uint64_t{1} << 32);
-    const bool a_vec = addend && v.addend_shape[last] != 1;
-    const bool m_vec = mult && v.mult_shape[last] != 1;
-    for (int d = 0; d < last && vec; ++d) {
-        if (a_vec) vec = a_stride[d] % E == 0;
-        if (vec && m_vec) vec = m_stride[d] % E == 0;
-    }
-    // LDS tile path: o = rank-2 is not next to the last dim in x but some
-    // other dim t is (x stride == L); both streams become contiguous runs.
-    if (vec && rank >= 3) {
-        const int o = rank - 2;
-        const int64_t L = (int64_t)v.shape[last];
-        int t = -1;
-        for (int d = 0; d < last; ++d)
-            if (d != o && v.strides[d] == L && v.shape[d] > 1) t = d;
-        const uint64_t vpu = v.shape[last] / E;
-        if (t >= 0 && v.strides[o] != L && v.shape[o] > 1 &&
-            (vpu == 1 || vpu == 2 || vpu == 4 || vpu == 8 || vpu == 16)) {
-            TileVecPlan plan{};
-            plan.rank = rank;
-            plan.o = o;
-            plan.t = t;
-            uint64_t ys = 1;
-            for (int d = last; d >= 0; --d) {
-                plan.shape[d] = v.shape[d];
-                plan.x_stride[d] = v.strides[d];
-                plan.a_stride[d] = a_stride[d];
-                plan.m_stride[d] = m_stride[d];
-                plan.y_stride[d] = ys;
-                ys *= v.shape[d];
-            }
-            plan.x_offset = v.offset;
-            plan.tiles_o = (uint32_t)((v.shape[o] + kTileUnits - 1) / kTileUnits);
-            plan.tiles_t = (uint32_t)((v.shape[t] + kTileUnits - 1) / kTileUnits);
-            plan.a_vec = a_vec;
-            plan.m_vec = m_vec;
-            const uint64_t batches = n / (v.shape[o] * v.shape[t] * v.shape[last]);
-            const uint64_t blocks = batches * plan.tiles_o * plan.tiles_t;
-            if (blocks < (uint64_t{1} << 31)) {
-                const dim3 grid((unsigned)blocks), block(kBlock);
-                switch (vpu) {
-                    case 1: hipLaunchKernelGGL((view_tile_vec_kernel<S, 1>), grid, block, 0, s, x, addend, mult, y, plan); break;
-                    case 2: hipLaunchKernelGGL((view_tile_vec_kernel<S, 2>), grid, block, 0, s, x, addend, mult, y, plan); break;
-                    case 4: hipLaunchKernelGGL((view_tile_vec_kernel<S, 4>), grid, block, 0, s, x, addend, mult, y, plan); break;
-                    case 8: hipLaunchKernelGGL((view_tile_vec_kernel<S, 8>), grid, block, 0, s, x, addend, mult, y, plan); break;
-                    default: hipLaunchKernelGGL((view_tile_vec_kernel<S, 16>), grid, block, 0, s, x, addend, mult, y, plan); break;
-                }
-                return hipGetLastError();
-            }
+    GatherPlan gp;
+    uint32_t blocks = 0;
+    if (aligned16(x) && aligned16(y) && aligned16(addend) && aligned16(mult) &&
+        gather_plan<S>(c, v.offset, n, addend != nullptr, mult != nullptr, &gp, &blocks)) {
+        const int ka = !addend ? kNone : c.a_stride[last] != 0 ? kVector : kScalar;
+        const int km = !mult ? kNone : c.m_stride[last] != 0 ? kVector : kScalar;
+        const dim3 grid(blocks), block(kBlock);
+#define ICSDK_GATHER(A, M)                                                                      \
+    hipLaunchKernelGGL((view_gather_kernel<S, A, M>), grid, block, 0, s, x, addend, mult, y, gp)
+        switch (ka * 3 + km) {
+            case 0: ICSDK_GATHER(kNone, kNone); break;
+            case 1: ICSDK_GATHER(kNone, kVector); break;
+            case 2: ICSDK_GATHER(kNone, kScalar); break;
+            case 3: ICSDK_GATHER(kVector, kNone); break;
+            case 4: ICSDK_GATHER(kVector, kVector); break;
+            case 5: ICSDK_GATHER(kVector, kScalar); break;
+            case 6: ICSDK_GATHER(kScalar, kNone); break;
+            case 7: ICSDK_GATHER(kScalar, kVector); break;
+            default: ICSDK_GATHER(kScalar, kScalar); break;
         }
-    }
-    if (vec) {
-        ViewPlan plan{};
-        plan.rank = rank;
-        for (int d = 0; d < rank; ++d) {
-            const uint64_t extent = d == last ? v.shape[d] / E : v.shape[d];
-            plan.dims[d] = make_fast_div((uint32_t)extent);
-            plan.x_stride[d] = v.strides[d];
-            plan.a_stride[d] = a_stride[d];
-            plan.m_stride[d] = m_stride[d];
-        }
-        plan.x_offset = v.offset;
-        plan.a_vec = a_vec;
-        plan.m_vec = m_vec;
-        const uint64_t nvec = n / E;
-        uint64_t grid = (nvec + kBlock * 4 - 1) / (kBlock * 4);
-        if (grid > (1u << 20)) grid = 1u << 20;
-        hipLaunchKernelGGL((view_vec_kernel<S>), dim3((unsigned)grid), dim3(kBlock), 0, s, x,
-                           addend, mult, y, (uint32_t)nvec, plan);
+#undef ICSDK_GATHER
         return hipGetLastError();
     }
 
-    // tile path: exactly one view dim p != last has x stride 1
+    // tile path: exactly one coalesced dim p != last has x stride 1
     int p = -1;
     for (int d = 0; d < last; ++d)
-        if (v.strides[d] == 1 && v.shape[d] > 1) p = p < 0 ? d : -2;
-    if (p >= 0 && v.strides[last] != 1 && v.shape[last] > 1) {
+        if (c.x_stride[d] == 1) p = p < 0 ? d : -2;
+    if (p >= 0 && c.x_stride[last] != 1) {
         TilePlan plan{};
-        plan.rank = rank;
+        plan.rank = c.rank;
         plan.p = p;
         uint64_t ys = 1;
         for (int d = last; d >= 0; --d) {
-            plan.shape[d] = v.shape[d];
-            plan.x_stride[d] = v.strides[d];
-            plan.a_stride[d] = a_stride[d];
-            plan.m_stride[d] = m_stride[d];
+            plan.shape[d] = c.shape[d];
+            plan.x_stride[d] = c.x_stride[d];
+            plan.a_stride[d] = c.a_stride[d];
+            plan.m_stride[d] = c.m_stride[d];
             plan.y_stride[d] = ys;
-            ys *= v.shape[d];
+            ys *= c.shape[d];
         }
         plan.x_offset = v.offset;
-        plan.batches = n / (v.shape[p] * v.shape[last]);
-        plan.tiles_p = (uint32_t)((v.shape[p] + kTile - 1) / kTile);
-        plan.tiles_l = (uint32_t)((v.shape[last] + kTile - 1) / kTile);
+        plan.batches = n / (c.shape[p] * c.shape[last]);
+        plan.tiles_p = (uint32_t)((c.shape[p] + kTile - 1) / kTile);
+        plan.tiles_l = (uint32_t)((c.shape[last] + kTile - 1) / kTile);
         const uint64_t blocks = plan.batches * plan.tiles_p * plan.tiles_l;
         if (blocks < (uint64_t{1} << 31)) {
             hipLaunchKernelGGL((view_tile_kernel<S>), dim3((unsigned)blocks), dim3(kBlock), 0,
@@ -452,12 +395,12 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend, const 
     }
 
     ScalarPlan plan{};
-    plan.rank = rank;
-    for (int d = 0; d < rank; ++d) {
-        plan.shape[d] = v.shape[d];
-        plan.x_stride[d] = v.strides[d];
-        plan.a_stride[d] = a_stride[d];
-        plan.m_stride[d] = m_stride[d];
+    plan.rank = c.rank;
+    for (int d = 0; d < c.rank; ++d) {
+        plan.shape[d] = c.shape[d];
+        plan.x_stride[d] = c.x_stride[d];
+        plan.a_stride[d] = c.a_stride[d];
+        plan.m_stride[d] = c.m_stride[d];
     }
     plan.x_offset = v.offset;
     uint64_t grid = (n + kBlock * 4 - 1) / (kBlock * 4);

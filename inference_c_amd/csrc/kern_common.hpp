@@ -64,6 +64,36 @@ __device__ inline void store16_stream(T *p, const Vec16<T> &value) {
                                 reinterpret_cast<u32x4 *>(p));
 }
 
+// ---- write-through stores (buffer_store_dwordx4 ... sc1) -----------------
+
+// Word 3 of a raw (untyped) buffer resource on gfx9-family parts:
+// DATA_FORMAT = 32-bit, everything else zero.
+constexpr int kRawBufferWord3 = 0x00020000;
+// Cache policy of a store with device scope (SC1): the line is written
+// through this XCD's L2 towards memory instead of being left dirty in it.
+constexpr int kPolicyDeviceScope = 16;
+
+// A window of at most 4 GiB of output, addressed by 32-bit byte offsets from
+// a base that is the same for every lane of the wave (a kernel argument plus
+// block-uniform terms: the descriptor lives in scalar registers). Stores at
+// or past `range` bytes are dropped by the hardware's range check.
+//
+// Used for outputs that the kernel never reads back: on MI355X a gather or a
+// row kernel whose stores write through L2 finishes sooner than the same
+// kernel with non-temporal stores, which leave dirty lines for the
+// end-of-kernel writeback.
+struct OutWindow {
+    __amdgpu_buffer_rsrc_t rsrc;
+    __device__ OutWindow(void *uniform_base, uint32_t range)
+        : rsrc(__builtin_amdgcn_make_buffer_rsrc(uniform_base, 0, (int)range, kRawBufferWord3)) {}
+
+    template <typename T>
+    __device__ inline void store16(uint32_t byte_offset, const Vec16<T> &value) const {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, value), rsrc,
+                                               (int)byte_offset, 0, kPolicyDeviceScope);
+    }
+};
+
 // ---- fast math for f16-output paths ---------------------------------------
 
 // e^x through v_exp_f32 (2^x). The product x*log2(e) is rounded once, so the

@@ -82,16 +82,17 @@ def test_config4_permuted_broadcast(sdk, orc, device):
 
 
 @pytest.mark.parametrize("case", ["vector_tile", "vector_tile_ragged", "vector_rows", "tile",
-                                  "scalar", "broadcast_x", "offset", "rank1"])
+                                  "scalar", "broadcast_x", "offset", "rank1", "coalesce_contig",
+                                  "rank6", "unit_dims", "one_vector_runs", "addend_inner_bcast"])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_view_paths(sdk, orc, case, dtype):
     dt = "f16" if dtype == "f16" else "f32"
-    if case == "vector_tile":  # (0,2,1,3) permutation: LDS-staged 8x8 unit tiles
+    if case == "vector_tile":  # (0,2,1,3) permutation, 16-element runs
         x = orc.normal((3, 40, 5, 16), 52, 0, 0.0, 1.0, dt)
         shape, strides, off = (3, 5, 40, 16), (3200, 16, 80, 1), 0
         A = orc.uniform((1, 5, 1, 16), 52, 1, -1, 1, dt)
         M = orc.uniform((3, 1, 40, 1), 52, 2, -1, 1, dt)
-    elif case == "vector_tile_ragged":  # tile edges (13, 11 not multiples of 8), batch dims
+    elif case == "vector_tile_ragged":  # rank-5 permutation with odd extents
         x = orc.normal((2, 3, 13, 11, 32), 58, 0, 0.0, 1.0, dt)
         shape = (2, 3, 11, 13, 32)
         strides = (3 * 13 * 11 * 32, 13 * 11 * 32, 32, 11 * 32, 1)
@@ -121,6 +122,39 @@ def test_view_paths(sdk, orc, case, dtype):
         x = orc.normal((10, 48), 56, 0, 0.0, 1.0, dt)
         shape, strides, off = (4, 32), (96, 1), 8 if dt == "f16" else 4
         A, M = orc.uniform((1, 32), 56, 1, -1, 1, dt), orc.uniform((4, 32), 56, 2, -1, 1, dt)
+    elif case == "coalesce_contig":  # contiguous view: x and A merge to one dim, M splits it
+        x = orc.normal((3, 4, 5, 32), 60, 0, 0.0, 1.0, dt)
+        shape, strides, off = (3, 4, 5, 32), (640, 160, 32, 1), 0
+        A = orc.uniform((3, 4, 5, 32), 60, 1, -1, 1, dt)
+        M = orc.uniform((3, 4, 1, 1), 60, 2, -1, 1, dt)
+    elif case == "rank6":  # six dims that cannot merge: the any-rank gather kernel
+        x = orc.normal((2, 3, 2, 3, 2, 16), 61, 0, 0.0, 1.0, dt)
+        phys = (2, 3, 2, 3, 2, 16)
+        cstr = [1] * 6
+        for d in range(4, -1, -1):
+            cstr[d] = cstr[d + 1] * phys[d + 1]
+        perm = (4, 2, 0, 3, 1, 5)
+        shape = tuple(phys[p] for p in perm)
+        strides = tuple(cstr[p] for p in perm)
+        off = 0
+        A = orc.uniform((1,) + shape[1:], 61, 1, -1, 1, dt)
+        M = orc.uniform(shape[:5] + (1,), 61, 2, -1, 1, dt)
+    elif case == "unit_dims":  # extents of 1 between permuted dims
+        x = orc.normal((4, 1, 6, 1, 24), 62, 0, 0.0, 1.0, dt)
+        shape, strides, off = (6, 1, 4, 1, 24), (24, 999, 144, 5, 1), 0
+        A = orc.uniform((6, 1, 1, 1, 24), 62, 1, -1, 1, dt)
+        M = orc.uniform((1, 1, 4, 1, 1), 62, 2, -1, 1, dt)
+    elif case == "one_vector_runs":  # innermost run of exactly one 16-byte vector
+        e = 8 if dt == "f16" else 4
+        x = orc.normal((5, 7, 3, e), 63, 0, 0.0, 1.0, dt)
+        shape, strides, off = (5, 3, 7, e), (7 * 3 * e, e, 3 * e, 1), 0
+        A = orc.uniform((1, 3, 1, e), 63, 1, -1, 1, dt)
+        M = orc.uniform((5, 1, 7, 1), 63, 2, -1, 1, dt)
+    elif case == "addend_inner_bcast":  # addend a scalar per vector, multiplier a vector
+        x = orc.normal((6, 4, 32), 64, 0, 0.0, 1.0, dt)
+        shape, strides, off = (4, 6, 32), (32, 128, 1), 0
+        A = orc.uniform((4, 6, 1), 64, 1, -1, 1, dt)
+        M = orc.uniform((1, 6, 32), 64, 2, -1, 1, dt)
     else:
         x = orc.normal((100,), 57, 0, 0.0, 1.0, dt)
         shape, strides, off = (33,), (3,), 1
