@@ -11,8 +11,9 @@
 // block's rotations, angle = (float)((double)(offset + p) / denom[d]) and
 // sincosf, into LDS, and after one barrier every lane rotates its pairs in
 // f32 (left*c - right*s, right*c + left*s, no contraction) and stores both
-// vectors. Every q/k byte is read once and written once; the angles cost
-// `half` sincos per position, shared by all heads of the position.
+// vectors, written through L2 into the bytes they came from. Every q/k byte
+// is read once and written once; the angles cost `half` sincos per position,
+// shared by all heads of the position.
 //
 // Table path (other shapes): a table kernel computes the same (cos, sin) per
 // (position, pair) into device scratch, then one lane per pair rotates.
@@ -115,9 +116,13 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     const uint32_t rot_entries = npos * half;
     const uint32_t it0 = blockIdx.y * (uint32_t)(kIt * kBlock);
     Vec16<S> lv[kIt], rv[kIt];
-    S *row_ptr[kIt];
+    uint32_t off[kIt];   // element offset of the item's left vector in its q / k window
+    bool in_q[kIt];
     uint32_t slot[kIt];  // index of the item's first rotation in `rot`
     bool ok[kIt];
+    // block-uniform windows over this block's positions of q and of k
+    S *const q0 = q + (size_t)p0 * qh * (2 * half);
+    S *const k0 = k + (size_t)p0 * kh * (2 * half);
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
         const uint32_t raw = it0 + threadIdx.x + u * kBlock;
@@ -127,13 +132,12 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         const uint32_t rest = item - pp * per_pos;
         const uint32_t row = rest / kChunks;
         const uint32_t c = rest - row * kChunks;
-        const size_t p = (size_t)p0 + pp;
-        S *base = row < qh ? q + (p * qh + row) * (2 * half)
-                           : k + (p * kh + (row - qh)) * (2 * half);
-        row_ptr[u] = base + c * E;
+        in_q[u] = row < qh;
+        off[u] = (in_q[u] ? pp * qh + row : pp * kh + (row - qh)) * (2 * half) + c * E;
         slot[u] = pp * half + c * E;
-        lv[u] = load16_stream(row_ptr[u]);
-        rv[u] = load16_stream(row_ptr[u] + half);
+        const S *src = (in_q[u] ? q0 : k0) + off[u];
+        lv[u] = load16_stream(src);
+        rv[u] = load16_stream(src + half);
     }
     // The denominators go to LDS through scalar loads (uniform addresses,
     // counted by lgkmcnt), so computing the rotations never waits for the
@@ -152,6 +156,9 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         rot[e] = make_float2(c, sn);
     }
     __syncthreads();
+    // results go back through L2 (write-through stores) into the same bytes
+    const OutWindow q_out(q0, npos * qh * (2 * half) * (uint32_t)sizeof(S));
+    const OutWindow k_out(k0, npos * kh * (2 * half) * (uint32_t)sizeof(S));
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
         if (!ok[u]) continue;
@@ -163,8 +170,23 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
             lo.v[e] = Elem<S>::store(l * t.x - r * t.y);
             ro.v[e] = Elem<S>::store(r * t.x + l * t.y);
         }
-        store16_stream(row_ptr[u], lo);
-        store16_stream(row_ptr[u] + half, ro);
+        // The window is chosen per wave (a descriptor must be wave-uniform):
+        // a wave whose items all lie in q, or all in k, writes through its
+        // window; a wave that straddles the two uses ordinary stores.
+        const uint32_t bytes = off[u] * (uint32_t)sizeof(S);
+        const uint64_t active = __builtin_amdgcn_ballot_w64(true);
+        const uint64_t q_lanes = __builtin_amdgcn_ballot_w64(in_q[u]);
+        if (q_lanes == active) {
+            q_out.store16(bytes, lo);
+            q_out.store16(bytes + half * (uint32_t)sizeof(S), ro);
+        } else if (q_lanes == 0) {
+            k_out.store16(bytes, lo);
+            k_out.store16(bytes + half * (uint32_t)sizeof(S), ro);
+        } else {
+            S *dst = (in_q[u] ? q0 : k0) + off[u];
+            store16_stream(dst, lo);
+            store16_stream(dst + half, ro);
+        }
     }
 }
 
