@@ -104,22 +104,25 @@ __device__ inline Vec16<S> apply(const Vec16<S> &a, const Vec16<S> &b, Op op) {
 
 // One 16-byte vector per lane and a one-shot grid (one wave per KiB per
 // operand). Measured on MI355X this streams at the device's practical
-// ceiling (~6.1 TB/s for 128 MiB operands); deeper per-lane unrolling and
+// ceiling (~6.4 TB/s for 128 MiB operands); deeper per-lane unrolling and
 // persistent grid-stride loops were 5-20% slower, and cached (temporal)
 // loads ~40% slower. Vectors past the grid's coverage (grids are capped at
-// 2^31 - 1 blocks) are picked up by the stride loop.
-template <typename S, int kArity, class Op>
+// 2^31 - 1 blocks) are picked up by the stride loop, whose bound is
+// block-uniform. kThrough selects write-through stores (small outputs).
+template <typename S, int kArity, class Op, bool kThrough>
 __global__ __launch_bounds__(kBlock) void map_vec_kernel(const S *__restrict__ a,
                                                          const S *__restrict__ b,
                                                          S *__restrict__ y, size_t nvec,
                                                          size_t n, Op op) {
     constexpr int E = Vec16<S>::N;
     const size_t stride = (size_t)gridDim.x * kBlock;
-    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < nvec; i += stride) {
+    for (size_t first = (size_t)blockIdx.x * kBlock; first < nvec; first += stride) {
+        const size_t i = first + threadIdx.x;
+        if (i >= nvec) break;
         const Vec16<S> va = load16_stream(a + i * E);
         Vec16<S> vb{};
         if constexpr (kArity == 2) vb = load16_stream(b + i * E);
-        store16_stream(y + i * E, apply<S, kArity>(va, vb, op));
+        store_block_vec<kThrough>(y, first * E, apply<S, kArity>(va, vb, op));
     }
     // ragged tail (fewer than one vector)
     if (blockIdx.x == 0 && threadIdx.x < n - nvec * E) {
@@ -160,8 +163,12 @@ hipError_t launch_map(const S *a, const S *b, S *y, size_t n, hipStream_t s) {
     if (aligned16(a) && aligned16(b) && aligned16(y)) {
         const size_t nvec = n / E;
         const unsigned grid = grid_for(nvec > 0 ? nvec : 1, (size_t)kBlock);
-        hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op>), dim3(grid), dim3(kBlock), 0, s,
-                           a, b, y, nvec, n, Op{});
+        if (write_through_for(n * sizeof(S)))
+            hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, true>), dim3(grid), dim3(kBlock),
+                               0, s, a, b, y, nvec, n, Op{});
+        else
+            hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, false>), dim3(grid), dim3(kBlock),
+                               0, s, a, b, y, nvec, n, Op{});
     } else {
         hipLaunchKernelGGL((map_scalar_kernel<S, kArity, Op>), dim3(grid_for(n, kBlock)),
                            dim3(kBlock), 0, s, a, b, y, n, Op{});
@@ -204,14 +211,16 @@ __device__ inline float bias_value(float x, float b) {
 // Vector path: width % E == 0 and 16-byte aligned operands, nvec < 2^32.
 // The column of vector i is i mod (width / E), computed with a multiply-high
 // division; the bias vector is re-read from L1/L2 (it is width*sizeof(S) bytes).
-template <typename S, bool kGelu>
+template <typename S, bool kGelu, bool kThrough>
 __global__ __launch_bounds__(kBlock) void bias_vec_kernel(const S *__restrict__ x,
                                                           const S *__restrict__ bias,
                                                           S *__restrict__ y, uint32_t nvec,
                                                           FastDiv per_row) {
     constexpr int E = Vec16<S>::N;
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < nvec; i += stride) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t first = (size_t)blockIdx.x * kBlock; first < nvec; first += stride) {
+        if (first + threadIdx.x >= nvec) break;
+        const uint32_t i = (uint32_t)(first + threadIdx.x);
         const uint32_t row = fast_div(i, per_row);
         const uint32_t col = i - row * per_row.divisor;
         const Vec16<S> vx = load16_stream(x + (size_t)i * E);
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(kBlock) void bias_vec_kernel(const S *__restrict__ 
         for (int e = 0; e < E; ++e)
             out.v[e] = Elem<S>::store(bias_value<S, kGelu>(Elem<S>::load(vx.v[e]),
                                                            Elem<S>::load(vb.v[e])));
-        store16_stream(y + (size_t)i * E, out);
+        store_block_vec<kThrough>(y, first * E, out);
     }
 }
 
@@ -245,9 +254,14 @@ hipError_t launch_bias(const S *x, const S *bias, S *y, size_t rows, size_t widt
     const size_t nvec = n / E;
     if (width % E == 0 && aligned16(x) && aligned16(bias) && aligned16(y) &&
         nvec < (size_t{1} << 32)) {
-        hipLaunchKernelGGL((bias_vec_kernel<S, kGelu>), dim3(grid_for(nvec, kBlock)),
-                           dim3(kBlock), 0, s, x, bias, y, (uint32_t)nvec,
-                           make_fast_div((uint32_t)(width / E)));
+        const dim3 grid(grid_for(nvec, kBlock)), block(kBlock);
+        const FastDiv per_row = make_fast_div((uint32_t)(width / E));
+        if (write_through_for(n * sizeof(S)))
+            hipLaunchKernelGGL((bias_vec_kernel<S, kGelu, true>), grid, block, 0, s, x, bias, y,
+                               (uint32_t)nvec, per_row);
+        else
+            hipLaunchKernelGGL((bias_vec_kernel<S, kGelu, false>), grid, block, 0, s, x, bias, y,
+                               (uint32_t)nvec, per_row);
     } else {
         hipLaunchKernelGGL((bias_scalar_kernel<S, kGelu>), dim3(grid_for(n, kBlock)),
                            dim3(kBlock), 0, s, x, bias, y, n, width);

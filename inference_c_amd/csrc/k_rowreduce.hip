@@ -226,22 +226,25 @@ __global__ __launch_bounds__(kBlock) void rms_norm_stream_kernel(
 
 // ---- LayerNorm -----------------------------------------------------------
 
-template <typename S, int NV, int WPR>
+// kScale / kBias: which affine parameters are present (compile time, so that
+// their loads are unconditional and issued first, like RMSNorm's weights).
+template <typename S, int NV, int WPR, bool kExact, bool kScale, bool kBias>
 __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
     const S *__restrict__ x, const S *__restrict__ scale, const S *__restrict__ bias,
     S *__restrict__ y, size_t rows, uint32_t width, float eps) {
     __shared__ float lds[kBlock / kWave];
-    using R = RowRegs<S, NV, WPR>;
+    using R = RowRegs<S, NV, WPR, kExact>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
     if (slot.row >= rows) return;
     const uint32_t vpr = width / E;
     const size_t base = slot.row * width;
+    Vec16<S> sv[NV], bv[NV];
+    if constexpr (kScale) load_params<S, NV, WPR, kExact>(scale, slot.t, vpr, sv);
+    if constexpr (kBias) load_params<S, NV, WPR, kExact>(bias, slot.t, vpr, bv);
+    __builtin_amdgcn_sched_barrier(0);
     R r;
     r.load(x + base, slot.t, vpr, 0.0f);
-    Vec16<S> sv[NV], bv[NV];
-    if (scale) load_params<S, NV, WPR>(scale, slot.t, vpr, sv);
-    if (bias) load_params<S, NV, WPR>(bias, slot.t, vpr, bv);
     float total = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
     float variance = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
-        if (r.valid(j, slot.t, vpr)) {
+        if (R::valid(j, slot.t, vpr)) {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const float d = r.v[j][e] - mean;
@@ -260,19 +263,20 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
         }
     variance = group_sum<WPR>(variance, lds);
     const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
+    const OutWindow out(y + base, width * (uint32_t)sizeof(S));
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
-        if (vi < vpr) {
-            Vec16<S> out;
+        if (R::valid(j, slot.t, vpr)) {
+            Vec16<S> o;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float v = (r.v[j][e] - mean) * inverse_std;
-                if (scale) v *= Elem<S>::load(sv[j].v[e]);
-                if (bias) v += Elem<S>::load(bv[j].v[e]);
-                out.v[e] = Elem<S>::store(v);
+                if constexpr (kScale) v *= Elem<S>::load(sv[j].v[e]);
+                if constexpr (kBias) v += Elem<S>::load(bv[j].v[e]);
+                o.v[e] = Elem<S>::store(v);
             }
-            store16_stream(y + base + (size_t)vi * E, out);
+            out.store16(vi * 16u, o);
         }
     }
 }
@@ -598,11 +602,29 @@ hipError_t launch_layer(const S *x, const S *scale, const S *bias, S *y, size_t 
     RowShape shape;
     const bool aligned = aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y);
     if (pick_row_shape(width, sizeof(S), aligned, &shape)) {
-#define ICSDK_LN(NV, WPR)                                                                  \
-    hipLaunchKernelGGL((layer_norm_kernel<S, NV, WPR>), row_grid(rows, WPR), dim3(kBlock), \
-                       0, s, x, scale, bias, y, rows, (uint32_t)width, eps)
+        const bool exact = width / (16 / sizeof(S)) == (size_t)shape.nv * shape.wpr * kWave;
+        const int affine = (scale ? 1 : 0) + (bias ? 2 : 0);
+#define ICSDK_LN_GO(NV, WPR, EX, SC, BI)                                                    \
+    hipLaunchKernelGGL((layer_norm_kernel<S, NV, WPR, EX, SC, BI>), row_grid(rows, WPR),     \
+                       dim3(kBlock), 0, s, x, scale, bias, y, rows, (uint32_t)width, eps)
+#define ICSDK_LN_AFF(NV, WPR, EX)                                                           \
+    do {                                                                                    \
+        switch (affine) {                                                                   \
+            case 0: ICSDK_LN_GO(NV, WPR, EX, false, false); break;                          \
+            case 1: ICSDK_LN_GO(NV, WPR, EX, true, false); break;                           \
+            case 2: ICSDK_LN_GO(NV, WPR, EX, false, true); break;                           \
+            default: ICSDK_LN_GO(NV, WPR, EX, true, true); break;                           \
+        }                                                                                   \
+    } while (0)
+#define ICSDK_LN(NV, WPR)                                                                   \
+    do {                                                                                    \
+        if (exact) ICSDK_LN_AFF(NV, WPR, true);                                             \
+        else ICSDK_LN_AFF(NV, WPR, false);                                                  \
+    } while (0)
         ICSDK_ROW_DISPATCH(shape, ICSDK_LN);
 #undef ICSDK_LN
+#undef ICSDK_LN_AFF
+#undef ICSDK_LN_GO
     } else {
         hipLaunchKernelGGL((layer_norm_stream_kernel<S>), dim3((unsigned)rows), dim3(kBlock),
                            0, s, x, scale, bias, y, rows, width, eps);

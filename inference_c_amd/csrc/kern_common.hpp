@@ -94,6 +94,25 @@ struct OutWindow {
     }
 };
 
+// Which store a streaming kernel uses for an output of `bytes` bytes. Measured
+// on MI355X with a three-stream f32 add: writing through L2 is 1-5% faster up
+// to 64 MiB of output and ~1.5% slower from 128 MiB, where non-temporal stores
+// win.
+constexpr size_t kWriteThroughMaxBytes = size_t{96} << 20;
+inline bool write_through_for(size_t bytes) { return bytes <= kWriteThroughMaxBytes; }
+
+// Stores one 16-byte vector of a block's contiguous output span: element
+// `block_first + threadIdx.x * N` of `y`, where block_first is block-uniform.
+template <bool kThrough, typename T>
+__device__ inline void store_block_vec(T *y, size_t block_first, const Vec16<T> &value) {
+    if constexpr (kThrough) {
+        const OutWindow w(y + block_first, kBlock * 16u);
+        w.store16(threadIdx.x * 16u, value);
+    } else {
+        store16_stream(y + block_first + (size_t)threadIdx.x * Vec16<T>::N, value);
+    }
+}
+
 // ---- fast math for f16-output paths ---------------------------------------
 
 // e^x through v_exp_f32 (2^x). The product x*log2(e) is rounded once, so the

@@ -69,11 +69,11 @@ def test_residual_rms_norm_f16(sdk, orc, rows, width, device):
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 @pytest.mark.parametrize("rows,width", [(3, 64), (37, 2048), (2, 1001), (3, 8192)])
-@pytest.mark.parametrize("affine", ["none", "scale", "both"])
+@pytest.mark.parametrize("affine", ["none", "scale", "bias", "both"])
 def test_layer_norm(sdk, orc, dtype, rows, width, affine):
     x = orc.normal((rows, width), 24, 0, 0.5, 2.0, dtype)
-    s = orc.uniform((width,), 24, 1, 0.5, 1.5, dtype) if affine != "none" else None
-    b = orc.uniform((width,), 24, 2, -1.0, 1.0, dtype) if affine == "both" else None
+    s = orc.uniform((width,), 24, 1, 0.5, 1.5, dtype) if affine in ("scale", "both") else None
+    b = orc.uniform((width,), 24, 2, -1.0, 1.0, dtype) if affine in ("bias", "both") else None
     tx, ts, tb = tensors(sdk, [x, s, b])
     ty = sdk.tensor(dtype, x.shape)
     sdk.call(f"tensor_layer_norm_{dtype}", tx, ts, tb, 1e-5, ty)
