@@ -7,6 +7,8 @@
 // Host-pointer slots are synchronous: operands are staged through the device
 // pool (reused across calls, released by release_cache), the kernel runs on
 // the SDK stream and the outputs are copied back before the slot returns.
+// The embedding slots keep their table uploaded per host address, as the
+// CUDA backend does, until release_cache.
 // *_device slots take raw device addresses and only enqueue. Argument checks
 // mirror the CUDA wrappers (non-null pointers, nonzero sizes, no size_t
 // overflow); a failed check returns 0.
@@ -228,7 +230,43 @@ int rope32(float *q, float *k, size_t s, size_t qh, size_t kh, size_t d, double 
 }
 int argmax16(const uint16_t *x, size_t n, uint32_t *r) { return host_argmax(x, n, r); }
 int argmax32(const float *x, size_t n, uint32_t *r) { return host_argmax(x, n, r); }
-void release_cache(void) { scratch_clear(); }
+
+// Compute-table embedding slots (CUDA: tensor_compute_cuda.cu:484-495): the
+// table is uploaded once per host address (weight cache), the ids and the
+// output are staged; an id at or past table_rows gives a zero row.
+template <typename T>
+int host_embedding(const T *table, const uint32_t *ids, T *out, size_t rows, size_t width,
+                   size_t table_rows) {
+    size_t n, table_n;
+    if (table == nullptr || ids == nullptr || out == nullptr || rows == 0 || width == 0 ||
+        table_rows == 0 || !product(rows, width, &n) || !product(table_rows, width, &table_n) ||
+        !count_ok<T>(n) || !count_ok<T>(table_n) || !count_ok<uint32_t>(rows))
+        return 0;
+    Staging st("hip backend", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const void *device_table = weight_cache_get(table, table_n * sizeof(T));
+    if (device_table == nullptr) return 0;
+    const void *pi = st.in(ids, rows * sizeof(uint32_t));
+    void *po = st.out(out, n * sizeof(T));
+    if (st.failed()) return 0;
+    return st.finish(k::embedding_gather(TENSOR_DTYPE_U32, device_table, table_rows,
+                                         width * sizeof(T), sizeof(T), pi, rows, po,
+                                         st.stream()))
+               ? 1
+               : 0;
+}
+int embedding16(const uint16_t *t, const uint32_t *ids, uint16_t *o, size_t r, size_t w,
+                size_t tr) {
+    return host_embedding(t, ids, o, r, w, tr);
+}
+int embedding32(const float *t, const uint32_t *ids, float *o, size_t r, size_t w, size_t tr) {
+    return host_embedding(t, ids, o, r, w, tr);
+}
+
+void release_cache(void) {
+    scratch_clear();
+    weight_cache_clear();
+}
 
 // Device-resident slots: raw device addresses, enqueue only.
 int bias32_device(const void *x, const void *b, void *y, size_t rows, size_t width) {
@@ -275,6 +313,7 @@ extern "C" const TensorComputeBackend *tensor_compute_hip_backend(void) {
         b.silu_multiply_f16 = silu_mul16;
         b.residual_add_f16 = residual16;
         b.argmax_f16 = argmax16;
+        b.embedding_f16 = embedding16;
         b.rms_norm_f32 = rms32;
         b.layer_norm_f32 = layer32;
         b.bias_add_f32 = bias32;
@@ -283,6 +322,7 @@ extern "C" const TensorComputeBackend *tensor_compute_hip_backend(void) {
         b.silu_multiply_f32 = silu_mul32;
         b.residual_add_f32 = residual32;
         b.argmax_f32 = argmax32;
+        b.embedding_f32 = embedding32;
         b.release_cache = release_cache;
         b.bias_add_f32_device = bias32_device;
         b.bias_add_f16_device = bias16_device;

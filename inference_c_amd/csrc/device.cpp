@@ -139,6 +139,43 @@ void scratch_clear() {
     for (void *p : blocks) (void)hipFree(p);
 }
 
+namespace {
+std::mutex weights_mutex;
+std::map<const void *, std::pair<void *, size_t>> weights;
+}  // namespace
+
+void *weight_cache_get(const void *host, size_t bytes) {
+    if (host == nullptr || bytes == 0 || !state().ready) return nullptr;
+    std::lock_guard<std::mutex> lock(weights_mutex);
+    auto found = weights.find(host);
+    if (found != weights.end())
+        return found->second.second == bytes ? found->second.first : nullptr;
+    bind_device();
+    void *device = nullptr;
+    if (hipMalloc(&device, bytes) != hipSuccess) return nullptr;
+    if (hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, state().stream) !=
+        hipSuccess) {
+        (void)hipStreamSynchronize(state().stream);
+        (void)hipFree(device);
+        return nullptr;
+    }
+    weights.emplace(host, std::make_pair(device, bytes));
+    return device;
+}
+
+void weight_cache_clear() {
+    std::vector<void *> blocks;
+    {
+        std::lock_guard<std::mutex> lock(weights_mutex);
+        for (auto &entry : weights) blocks.push_back(entry.second.first);
+        weights.clear();
+    }
+    if (blocks.empty() || !state().ready) return;
+    bind_device();
+    (void)hipStreamSynchronize(state().stream);
+    for (void *p : blocks) (void)hipFree(p);
+}
+
 std::mutex &grid_reduce_mutex() {
     static std::mutex m;
     return m;

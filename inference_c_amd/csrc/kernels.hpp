@@ -95,6 +95,17 @@ hipError_t view_add_mul_f32(const float *x, const ViewArgs &v, const float *adde
 hipError_t view_add_mul_f16(const uint16_t *x, const ViewArgs &v, const uint16_t *addend,
                             const uint16_t *mult, uint16_t *y, hipStream_t s);
 
+// Embedding lookup: out[i, :] = table[ids[i], :] (rows of row_bytes bytes,
+// elements of elem_bytes = 2 or 4). ids are I16/U16/I32/U32/I64/U64; an id
+// that is negative or >= table_rows gives a zero row. embedding_check writes
+// 1 to the device word `flag` when any id is such, else 0 (one block).
+bool embedding_index_type(TensorDType dtype);
+hipError_t embedding_check(TensorDType index_dtype, const void *ids, size_t count,
+                           uint64_t table_rows, uint32_t *flag, hipStream_t s);
+hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t table_rows,
+                            size_t row_bytes, size_t elem_bytes, const void *ids, size_t count,
+                            void *out, hipStream_t s);
+
 // Synthetic inputs (counter-based splitmix64).
 hipError_t fill_uniform(TensorDType dtype, void *y, size_t n, uint64_t seed,
                         uint64_t stream, float low, float high, hipStream_t s);

@@ -468,10 +468,102 @@ int fill(bool normal, TensorBuffer *t, uint64_t seed, uint64_t stream, float a, 
     return st.finish(status) ? 1 : 0;
 }
 
+// ---- embedding lookup (reference src/common/tensor_ops.c:41-161) ----------
+
+// Reads index `i` of a host index buffer as the reference does (:41-84):
+// false for a non-index dtype or a negative signed value.
+bool host_index(Buf indices, size_t i, uint64_t *id) {
+    const unsigned char *p = static_cast<const unsigned char *>(tensor_buffer_data(indices));
+    switch (tensor_buffer_dtype(indices)) {
+        case TENSOR_DTYPE_I16: { int16_t v; std::memcpy(&v, p + i * 2, 2); *id = (uint64_t)v; return v >= 0; }
+        case TENSOR_DTYPE_U16: { uint16_t v; std::memcpy(&v, p + i * 2, 2); *id = v; return true; }
+        case TENSOR_DTYPE_I32: { int32_t v; std::memcpy(&v, p + i * 4, 4); *id = (uint64_t)v; return v >= 0; }
+        case TENSOR_DTYPE_U32: { uint32_t v; std::memcpy(&v, p + i * 4, 4); *id = v; return true; }
+        case TENSOR_DTYPE_I64: { int64_t v; std::memcpy(&v, p + i * 8, 8); *id = (uint64_t)v; return v >= 0; }
+        case TENSOR_DTYPE_U64: std::memcpy(id, p + i * 8, 8); return true;
+        default: return false;
+    }
+}
+
+int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *out, char *error,
+                     size_t capacity) {
+    const bool f32 = dtype == TENSOR_DTYPE_F32;
+    // the F32 entry point also insists on an index dtype up front; the F16
+    // one finds a non-index dtype when it reads the first index (:86-101,
+    // :130-152)
+    if (!is(table, dtype) || !is(out, dtype) || indices == nullptr ||
+        tensor_buffer_rank(table) != 2 || tensor_buffer_rank(indices) != 1 ||
+        tensor_buffer_rank(out) != 2 ||
+        (f32 && !k::embedding_index_type(tensor_buffer_dtype(indices)))) {
+        set_error(error, capacity, "embedding lookup requires a rank-2 %s table, integer rank-1 "
+                  "indices, and rank-2 %s output", f32 ? "F32" : "F16", f32 ? "F32" : "F16");
+        return 0;
+    }
+    const uint64_t *ts = tensor_buffer_shape(table), *os = tensor_buffer_shape(out);
+    const size_t count = tensor_buffer_element_count(indices);
+    if (ts[0] == 0 || ts[1] == 0 || os[0] != count || os[1] != ts[1]) {
+        set_error(error, capacity, "embedding table and output dimensions do not match");
+        return 0;
+    }
+    bool host;
+    if (!common_storage({table, indices, out}, &host))
+        return storage_error("embedding lookup", error, capacity);
+    if (count == 0) return 1;
+    const char *bad_index = "embedding index is negative or outside the table";
+    const TensorDType index_dtype = tensor_buffer_dtype(indices);
+    if (!k::embedding_index_type(index_dtype)) {
+        set_error(error, capacity, "%s", bad_index);
+        return 0;
+    }
+    // every index is checked before any row is written: on the host for host
+    // buffers, by a one-block kernel (and one wait) for device buffers
+    if (host) {
+        for (size_t i = 0; i < count; ++i) {
+            uint64_t id;
+            if (!host_index(indices, i, &id) || id >= ts[0]) {
+                set_error(error, capacity, "%s", bad_index);
+                return 0;
+            }
+        }
+    }
+    Staging st("embedding lookup", host, error, capacity);
+    if (!st.begin()) return 0;
+    if (!host) {
+        ScratchBlock flag(sizeof(uint32_t));
+        uint32_t bad = 1;
+        if (flag.get() == nullptr) {
+            set_error(error, capacity, "embedding lookup: out of device memory");
+            return 0;
+        }
+        if (!hip_ok(k::embedding_check(index_dtype, tensor_buffer_device_handle_internal(indices),
+                                       count, ts[0], static_cast<uint32_t *>(flag.get()),
+                                       st.stream()),
+                    "embedding lookup: index check launch", error, capacity) ||
+            !hip_ok(hipMemcpyAsync(&bad, flag.get(), sizeof bad, hipMemcpyDeviceToHost,
+                                   st.stream()),
+                    "embedding lookup: index check read-back", error, capacity) ||
+            !hip_ok(hipStreamSynchronize(st.stream()), "embedding lookup: hipStreamSynchronize",
+                    error, capacity))
+            return 0;
+        if (bad) {
+            set_error(error, capacity, "%s", bad_index);
+            return 0;
+        }
+    }
+    const void *pt = src(st, table);
+    const void *pi = src(st, indices);
+    void *po = dst(st, out);
+    if (st.failed()) return 0;
+    const size_t elem = f32 ? 4 : 2;
+    const hipError_t status = k::embedding_gather(index_dtype, pt, ts[0], (size_t)ts[1] * elem,
+                                                  elem, pi, count, po, st.stream());
+    return st.finish(status) ? 1 : 0;
+}
+
 int out_of_scope(const char *op, char *error, size_t capacity) {
     set_error(error, capacity,
-              "%s is not provided by the HIP tensor-ops library (GEMM and gather work are "
-              "outside its scope)", op);
+              "%s is not provided by the HIP tensor-ops library (GEMM work is outside its "
+              "scope)", op);
     return 0;
 }
 
@@ -493,11 +585,13 @@ int tensor_linear_f32(Buf, Buf, Buf, TensorBuffer *, char *error, size_t capacit
 int tensor_linear_f16(Buf, Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
     return out_of_scope("tensor_linear_f16", error, capacity);
 }
-int tensor_embedding_lookup_f32(Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_embedding_lookup_f32", error, capacity);
+int tensor_embedding_lookup_f32(Buf table, Buf indices, TensorBuffer *output, char *error,
+                                size_t capacity) {
+    return embedding_lookup(TENSOR_DTYPE_F32, table, indices, output, error, capacity);
 }
-int tensor_embedding_lookup_f16(Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_embedding_lookup_f16", error, capacity);
+int tensor_embedding_lookup_f16(Buf table, Buf indices, TensorBuffer *output, char *error,
+                                size_t capacity) {
+    return embedding_lookup(TENSOR_DTYPE_F16, table, indices, output, error, capacity);
 }
 
 int tensor_rms_norm_f32(Buf input, Buf weight, float epsilon, TensorBuffer *output,

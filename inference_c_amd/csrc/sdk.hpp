@@ -33,6 +33,15 @@ void *scratch_acquire(size_t bytes);
 void scratch_release(void *ptr, size_t bytes);
 void scratch_clear();
 
+// Device copies of host tables passed to the compute-table slots, keyed by
+// host address like the CUDA backend's weight cache
+// (src/platform/cuda/tensor_compute_cuda.cu:24-50): the first call uploads
+// `bytes` bytes (enqueued on the SDK stream), later calls with the same
+// address reuse the copy, a call with the same address and another size
+// fails (nullptr), and weight_cache_clear() frees them (release_cache).
+void *weight_cache_get(const void *host, size_t bytes);
+void weight_cache_clear();
+
 // A pool block held for the duration of one call. Returning it to the pool
 // right after the launches is safe: every later user of the block enqueues
 // on the same SDK stream, after this call's kernels.

@@ -206,7 +206,10 @@ class Sdk:
                    device: bool = True) -> Tensor:
         if dtype is None:
             dtype = {np.dtype(np.float32): "f32", np.dtype(np.float16): "f16",
-                     np.dtype(np.float64): "f64", np.dtype(np.uint32): "u32"}[array.dtype]
+                     np.dtype(np.float64): "f64", np.dtype(np.int16): "i16",
+                     np.dtype(np.uint16): "u16", np.dtype(np.int32): "i32",
+                     np.dtype(np.uint32): "u32", np.dtype(np.int64): "i64",
+                     np.dtype(np.uint64): "u64"}[array.dtype]
         return self.tensor(dtype, array.shape, device).upload(array)
 
     def call(self, name: str, *args) -> None:

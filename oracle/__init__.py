@@ -56,7 +56,14 @@ _SIGS = {
     "orc_rope_f16": ([_P, _P, _Z, _Z, _Z, _Z, _D, _Z], None),
     "orc_view_add_mul_f16": ([_P, _Z, _P, _P, _U64, _P, _P, _P, _P, _P], None),
     "orc_view_add_mul_f32": ([_P, _Z, _P, _P, _U64, _P, _P, _P, _P, _P], None),
+    "orc_embedding_lookup": ([_P, _Z, _Z, _P, _I, _Z, _P], _I),
+    "orc_embedding_gather_u32": ([_P, _Z, _Z, _P, _Z, _P], None),
 }
+
+# TensorDType numbering (include/safetensors.h) of numpy index and value types
+INDEX_DTYPES = {np.dtype(np.int16): 4, np.dtype(np.uint16): 5, np.dtype(np.int32): 6,
+                np.dtype(np.uint32): 7, np.dtype(np.int64): 8, np.dtype(np.uint64): 9,
+                np.dtype(np.float16): 12, np.dtype(np.float32): 14}
 
 
 def _ptr(a: Optional[np.ndarray]):
@@ -259,6 +266,28 @@ class Oracle:
                                 _ptr(ad), _ptr(ash), _ptr(mu), _ptr(msh), out.ctypes.data)
         return out.view(np.float16) if x.dtype == np.float16 else out
 
+    def embedding_lookup(self, table, indices):
+        """Rows of `table` [rows, width] picked by `indices` (any numpy dtype;
+        the reference accepts int16/uint16/int32/uint32/int64/uint64), or
+        None when the reference would fail (an index unreadable, negative or
+        outside the table)."""
+        t = np.ascontiguousarray(table)
+        ids = np.ascontiguousarray(indices)
+        out = np.zeros((ids.size, t.shape[1]), t.dtype)
+        ok = self.lib.orc_embedding_lookup(t.ctypes.data, t.shape[0], t.shape[1] * t.itemsize,
+                                           ids.ctypes.data, INDEX_DTYPES.get(ids.dtype, 0),
+                                           ids.size, out.ctypes.data)
+        return out if ok else None
+
+    def embedding_gather_u32(self, table, ids):
+        """Compute-table slot semantics: uint32 ids, zero rows past the table."""
+        t = np.ascontiguousarray(table)
+        i = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty((i.size, t.shape[1]), t.dtype)
+        self.lib.orc_embedding_gather_u32(t.ctypes.data, t.shape[0], t.shape[1] * t.itemsize,
+                                          i.ctypes.data, i.size, out.ctypes.data)
+        return out
+
 
 class Reference:
     """The reference's portable C path (oracle/_ref/libref.so), driven through
@@ -294,6 +323,8 @@ class Reference:
         for name in ("tensor_silu_f32", "tensor_silu_f16"):
             getattr(lib, name).argtypes = [_P, _P, ctypes.c_char_p, _Z]
         lib.tensor_residual_add_f16.argtypes = [_P, _P, _P, ctypes.c_char_p, _Z]
+        for name in ("tensor_embedding_lookup_f32", "tensor_embedding_lookup_f16"):
+            getattr(lib, name).argtypes = [_P, _P, _P, ctypes.c_char_p, _Z]
         self.lib = lib
 
     def _make(self, dtype, array):
@@ -392,6 +423,27 @@ class Reference:
             for h in (hq, hk, hv, hm, ho):
                 self.lib.tensor_buffer_free(h)
             self.lib.tensor_workspace_free(ws)
+
+    def embedding_lookup(self, table, indices):
+        """tensor_embedding_lookup_f32/f16 on host buffers: (ok, rows, message)."""
+        dtype = "f16" if table.dtype == np.float16 else "f32"
+        ids = np.ascontiguousarray(indices)
+        shape = (ctypes.c_uint64 * 1)(ids.size)
+        hi = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(256)
+        assert self.lib.tensor_buffer_create(INDEX_DTYPES[ids.dtype], shape, 1, ctypes.byref(hi),
+                                             err, 256), err.value
+        if ids.nbytes:
+            ctypes.memmove(self.lib.tensor_buffer_data_mut(hi), ids.ctypes.data, ids.nbytes)
+        ht = self._make(dtype, table)
+        ho = self._make(dtype, np.zeros((ids.size, table.shape[1]), table.dtype))
+        try:
+            name = f"tensor_embedding_lookup_{dtype}"
+            ok = bool(getattr(self.lib, name)(ht, hi.value, ho, err, 256))
+            return ok, self._read(ho, (ids.size, table.shape[1]), dtype), err.value.decode()
+        finally:
+            for h in (ht, hi.value, ho):
+                self.lib.tensor_buffer_free(h)
 
     def convert(self, array, src, dst):
         h = self._make(src, array)

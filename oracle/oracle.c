@@ -597,3 +597,52 @@ void orc_view_add_mul_f32(const float *x, size_t rank, const uint64_t *shape,
         y[i] = v;
     }
 }
+
+/* ---- embedding lookup ---------------------------------------------------- */
+
+/* Index reading follows src/common/tensor_ops.c:41-84: I16/U16/I32/U32/I64/
+   U64 only (TensorDType numbering 4..9), signed values below zero rejected. */
+static int read_index(const void *indices, int dtype, size_t position, uint64_t *out) {
+    const unsigned char *p = (const unsigned char *)indices;
+    switch (dtype) {
+        case 4: { int16_t v; memcpy(&v, p + position * 2, 2); if (v < 0) return 0; *out = (uint64_t)v; return 1; }
+        case 5: { uint16_t v; memcpy(&v, p + position * 2, 2); *out = v; return 1; }
+        case 6: { int32_t v; memcpy(&v, p + position * 4, 4); if (v < 0) return 0; *out = (uint64_t)v; return 1; }
+        case 7: { uint32_t v; memcpy(&v, p + position * 4, 4); *out = v; return 1; }
+        case 8: { int64_t v; memcpy(&v, p + position * 8, 8); if (v < 0) return 0; *out = (uint64_t)v; return 1; }
+        case 9: { uint64_t v; memcpy(&v, p + position * 8, 8); *out = v; return 1; }
+        default: return 0;
+    }
+}
+
+/* Follows src/common/tensor_ops.c:86-161: every index is checked (readable,
+   not negative, below table_rows) before any row is written; then row i of
+   the output is a byte copy of table row indices[i]. */
+int orc_embedding_lookup(const void *table, size_t table_rows, size_t row_bytes,
+                         const void *indices, int index_dtype, size_t count, void *out) {
+    for (size_t i = 0; i < count; i++) {
+        uint64_t id;
+        if (!read_index(indices, index_dtype, i, &id) || id >= table_rows) return 0;
+    }
+    for (size_t i = 0; i < count; i++) {
+        uint64_t id = 0;
+        read_index(indices, index_dtype, i, &id);
+        memcpy((unsigned char *)out + i * row_bytes,
+               (const unsigned char *)table + (size_t)id * row_bytes, row_bytes);
+    }
+    return 1;
+}
+
+/* Follows the compute-table slot semantics of
+   src/platform/cuda/tensor_compute_cuda.cu:53-67: uint32 ids, an id at or
+   past table_rows yields a zero row. */
+void orc_embedding_gather_u32(const void *table, size_t table_rows, size_t row_bytes,
+                              const uint32_t *ids, size_t count, void *out) {
+    for (size_t i = 0; i < count; i++) {
+        unsigned char *dst = (unsigned char *)out + i * row_bytes;
+        if (ids[i] < table_rows)
+            memcpy(dst, (const unsigned char *)table + (size_t)ids[i] * row_bytes, row_bytes);
+        else
+            memset(dst, 0, row_bytes);
+    }
+}

@@ -125,6 +125,14 @@ void orc_view_add_mul_f32(const float *x, size_t rank, const uint64_t *shape,
                           const float *mult, const uint64_t *mult_shape,
                           float *y);
 
+/* embedding lookup: returns 1, or 0 (output untouched) when an index is
+   unreadable for its dtype (TensorDType numbering), negative or outside the
+   table; the compute-table variant zero-fills rows of out-of-range ids */
+int orc_embedding_lookup(const void *table, size_t table_rows, size_t row_bytes,
+                         const void *indices, int index_dtype, size_t count, void *out);
+void orc_embedding_gather_u32(const void *table, size_t table_rows, size_t row_bytes,
+                              const uint32_t *ids, size_t count, void *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,9 +81,11 @@ def test_out_of_scope_entry_points_fail_with_a_message(lib):
     from inference_c_amd import Sdk
     sdk = Sdk()
     a = sdk.tensor("f32", (2, 2), device=False)
-    for name in ("tensor_matmul_f32", "tensor_embedding_lookup_f16"):
+    for name in ("tensor_matmul_f32", "tensor_matmul_f16"):
         ok, msg = sdk.try_call(name, a, a, a)
         assert not ok and "not provided by the HIP tensor-ops library" in msg
+    ok, msg = sdk.try_call("tensor_linear_f16", a, a, None, a)
+    assert not ok and "not provided by the HIP tensor-ops library" in msg
     err = ctypes.create_string_buffer(256)
     res = ctypes.c_void_p(1)
     assert not lib.tensor_buffer_load(None, b"w", ctypes.byref(res), err, 256)
@@ -118,6 +120,49 @@ def test_validation_precedes_device_use(lib):
     for args, message in cases:
         ok, msg = sdk.try_call(*args)
         assert not ok and msg == message, (args[0], msg)
+
+
+def test_embedding_validation_matches_reference(lib, ref, orc):
+    """tensor_embedding_lookup_* reject bad operands and bad indices with the
+    reference's messages (src/common/tensor_ops.c:86-161) before any device
+    work: every index of a host call is checked on the host first."""
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    rows, width = 6, 4
+    for dtype, npt in (("f32", np.float32), ("f16", np.float16)):
+        table = orc.normal((rows, width), 18, 0, 0.0, 1.0, dtype)
+        t = sdk.from_numpy(table, device=False)
+        for ids in (np.array([1, -1, 2], np.int32), np.array([1, 6], np.uint16),
+                    np.array([0, 1 << 40], np.uint64), np.array([-5], np.int64)):
+            ti = sdk.from_numpy(ids, device=False)
+            out = sdk.tensor(dtype, (ids.size, width), device=False)
+            ok, msg = sdk.try_call(f"tensor_embedding_lookup_{dtype}", t, ti, out)
+            rok, _, rmsg = ref.embedding_lookup(table, ids)
+            assert not ok and not rok and msg == rmsg, (dtype, ids, msg, rmsg)
+        # dimension mismatch and a rank-2 index buffer
+        ti = sdk.from_numpy(np.array([0, 1], np.uint32), device=False)
+        bad_out = sdk.tensor(dtype, (3, width), device=False)
+        ok, msg = sdk.try_call(f"tensor_embedding_lookup_{dtype}", t, ti, bad_out)
+        assert not ok and msg == "embedding table and output dimensions do not match"
+        ti2 = sdk.from_numpy(np.zeros((2, 1), np.uint32), device=False)
+        out = sdk.tensor(dtype, (2, width), device=False)
+        ok, msg = sdk.try_call(f"tensor_embedding_lookup_{dtype}", t, ti2, out)
+        assert not ok and msg == (f"embedding lookup requires a rank-2 {dtype.upper()} table, "
+                                  f"integer rank-1 indices, and rank-2 {dtype.upper()} output")
+    # F32 checks the index dtype up front, F16 when it reads the first index
+    t32 = sdk.from_numpy(np.zeros((rows, width), np.float32), device=False)
+    tf = sdk.from_numpy(np.zeros(2, np.float32), device=False)
+    out = sdk.tensor("f32", (2, width), device=False)
+    ok, msg = sdk.try_call("tensor_embedding_lookup_f32", t32, tf, out)
+    assert not ok and "integer rank-1 indices" in msg
+    t16 = sdk.from_numpy(np.zeros((rows, width), np.float16), device=False)
+    out16 = sdk.tensor("f16", (2, width), device=False)
+    ok, msg = sdk.try_call("tensor_embedding_lookup_f16", t16, tf, out16)
+    assert not ok and msg == "embedding index is negative or outside the table"
+    # no indices: nothing to gather, success without a device
+    te = sdk.from_numpy(np.zeros(0, np.uint32), device=False)
+    empty = sdk.tensor("f16", (0, width), device=False)
+    assert sdk.try_call("tensor_embedding_lookup_f16", t16, te, empty)[0] == 1
 
 
 def test_empty_tensors_succeed_without_work(lib):

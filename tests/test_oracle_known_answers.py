@@ -117,3 +117,19 @@ def test_softmax_sdpa_known_answers(orc):
     # all masked -> zeros
     allm = np.full((2, 2), -np.inf, np.float32)
     assert np.all(orc.softmax(allm) == 0.0)
+
+
+def test_embedding_lookup_f32(orc):
+    # test_tensor_ops.c:62-82: ids {2, 0, 2} pick rows 2, 0, 2; id 4 of a
+    # 4-row table is rejected
+    table = np.array([0, 1, 2, 10, 11, 12, 20, 21, 22, 30, 31, 32], np.float32).reshape(4, 3)
+    got = orc.embedding_lookup(table, np.array([2, 0, 2], np.uint32))
+    assert got.ravel().tolist() == [20, 21, 22, 0, 1, 2, 20, 21, 22]
+    assert orc.embedding_lookup(table, np.array([2, 4, 2], np.uint32)) is None
+
+
+def test_embedding_compute_slot_f32(orc):
+    # test_tensor_compute.c:112-119 (embedding_f32 slot, uint32 ids)
+    table = np.arange(8, dtype=np.float32).reshape(4, 2)
+    got = orc.embedding_gather_u32(table, np.array([2, 0], np.uint32))
+    assert got.ravel().tolist() == [4, 5, 0, 1]

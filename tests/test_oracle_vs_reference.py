@@ -68,3 +68,46 @@ def test_softmax_special_rows_via_sdpa(orc, ref):
                   [-inf, 5, -inf, 5], [1e30, -1e30, 0, 1], [-inf, -inf, inf, -inf]], np.float32)
     for causal in (False, True):
         assert_bits_equal(orc.softmax(s, causal), ref.softmax_rows_f32(s, causal), "special rows")
+
+
+INDEX_TYPES = [np.int16, np.uint16, np.int32, np.uint32, np.int64, np.uint64]
+
+
+@pytest.mark.parametrize("index_type", INDEX_TYPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("case", ["valid", "negative", "past_end", "last_row", "empty"])
+def test_embedding_lookup(orc, ref, index_type, dtype, case):
+    """tensor_embedding_lookup_* (src/common/tensor_ops.c:86-161): outputs
+    and the accept/reject decision agree for every index dtype."""
+    rows, width = 37, 5
+    table = orc.normal((rows, width), 16, 0, 0.0, 1.0, dtype)
+    ids = (orc.uniform((23,), 16, 1, 0.0, rows - 0.001, "f32")).astype(np.int64)
+    if case == "negative":
+        if not np.issubdtype(index_type, np.signedinteger):
+            pytest.skip("unsigned indices cannot be negative")
+        ids[7] = -1
+    elif case == "past_end":
+        ids[11] = rows
+    elif case == "last_row":
+        ids[-1] = rows - 1
+    elif case == "empty":
+        ids = ids[:0]
+    ids = ids.astype(index_type)
+    ok, got, message = ref.embedding_lookup(table, ids)
+    want = orc.embedding_lookup(table, ids)
+    assert ok == (want is not None), message
+    if ok:
+        assert_bits_equal(want, got, "embedding")
+        assert_bits_equal(want, table[ids.astype(np.int64)], "embedding vs numpy take")
+    else:
+        assert message == "embedding index is negative or outside the table"
+
+
+def test_embedding_lookup_f16_rejects_float_indices(orc, ref):
+    """The F16 entry point does not check the index dtype up front: a
+    non-integer index buffer fails when its first index is read."""
+    table = orc.normal((4, 3), 17, 0, 0.0, 1.0, "f16")
+    ids = np.array([1.0, 2.0], np.float32)
+    ok, _, message = ref.embedding_lookup(table, ids)
+    assert not ok and message == "embedding index is negative or outside the table"
+    assert orc.embedding_lookup(table, ids) is None
