@@ -149,6 +149,7 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     fixed cost (launch, first-load latency, drain) keeps even a copy well
     under the 8 TB/s peak, and this is the ceiling a kernel of that size can
     be held to."""
+    import numpy as np
     from inference_c_amd import TensorView
     results = {}
     T = sdk.tensor
@@ -278,6 +279,20 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     measure("cfg5_residual_rms_norm_f16", cfg5, norm, 67_112_960, 8_388_608)
     measure("cfg5_rope_f16", cfg5, rope, 67_108_864, 16_777_216)
     measure("cfg5_swiglu_f16", cfg5, swiglu, 201_326_592, 33_554_432)
+    # embedding gather: a 32768-token prefill batch of int32 ids into
+    # a [32000, 2048] f16 table; device storage, so each call also runs the
+    # one-block index check and waits for its verdict before gathering
+    vocab, width, tokens = 32000, 2048, 32768
+    emb_table = filled("f16", (vocab, width), "normal", 6, 0, 0.0, 1.0)
+    def gather_set():
+        ids = T("i32", (tokens,))
+        host_ids = ((np.arange(tokens, dtype=np.int64) * 2654435761) % vocab).astype(np.int32)
+        ids.upload(host_ids)
+        return ids, T("f16", (tokens, width))
+    measure("embedding_lookup_f16", gather_set,
+            lambda s: sdk.call("tensor_embedding_lookup_f16", emb_table, s[0], s[1]),
+            2 * tokens * width * 2 + tokens * 4, tokens * width)
+    del emb_table
     # cfg5: global sum + max over 2^30 f32 U[-1,1], seed 0
     def cfg5_global():
         return filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0), T("f64", (1,)), T("f32", (1,))
@@ -330,8 +345,9 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one "
-                          "GPU and the path shards without communication (see DESIGN.md); "
-                          "run with --gpus 1"}))
+                          "GPU, and every op but the global reductions shards over rows or "
+                          "tokens with no communication, so the one-GPU figure is the per-GPU "
+                          "figure; run with --gpus 1"}))
         sys.exit(2)
 
     from inference_c_amd import Sdk

@@ -176,6 +176,37 @@ void weight_cache_clear() {
     for (void *p : blocks) (void)hipFree(p);
 }
 
+namespace {
+std::mutex words_mutex;
+std::vector<uint32_t *> free_words;
+constexpr size_t kWordsPerSlab = 1024;  // one 4 KiB page of pinned memory
+}  // namespace
+
+uint32_t *host_word_acquire() {
+    std::lock_guard<std::mutex> lock(words_mutex);
+    if (free_words.empty()) {
+        if (!state().ready) return nullptr;
+        bind_device();
+        void *slab = nullptr;
+        // coherent: a kernel's store is not held in a device cache; slabs stay
+        // allocated for the life of the process
+        if (hipHostMalloc(&slab, kWordsPerSlab * sizeof(uint32_t),
+                          hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+            return nullptr;
+        for (size_t i = 0; i < kWordsPerSlab; ++i)
+            free_words.push_back(static_cast<uint32_t *>(slab) + i);
+    }
+    uint32_t *word = free_words.back();
+    free_words.pop_back();
+    return word;
+}
+
+void host_word_release(uint32_t *word) {
+    if (word == nullptr) return;
+    std::lock_guard<std::mutex> lock(words_mutex);
+    free_words.push_back(word);
+}
+
 std::mutex &grid_reduce_mutex() {
     static std::mutex m;
     return m;

@@ -4,10 +4,12 @@
 // uint32, int64, uint64). Rows are moved as bytes, so one kernel serves every
 // element type.
 //
-// check  - one 1024-lane block scans the ids and writes 1 to `flag` when any
-//          is negative or at/past the table's row count, else 0 (the public
-//          entry points reject such calls before any row is written; one
-//          block needs no atomics and no pre-cleared flag);
+// check  - one 1024-lane block scans the ids (16-byte vectors, several in
+//          flight per lane) and writes 1 to `flag` when any is negative or
+//          at/past the table's row count, else 0 (the public entry points
+//          reject such calls before any row is written; one block needs no
+//          atomics and no pre-cleared flag, and `flag` may be pinned host
+//          memory, read after one stream wait);
 // gather - rows that are whole 16-byte vectors (and aligned): one output
 //          vector per lane on a one-shot grid; the lane's row and column
 //          come from a multiply-high division, its id from the (cached) id
@@ -33,18 +35,46 @@ __device__ inline bool index_ok(I value, uint64_t rows, uint64_t *id) {
 }
 
 constexpr int kCheckBlock = 1024;
+constexpr int kCheckUnroll = 4;  // 16-byte vectors in flight per lane
 
+// One block scans all ids: each lane keeps kCheckUnroll 16-byte vectors of
+// ids in flight per step (a 1024-lane block covers 64 KiB per step), then a
+// scalar tail; the verdict is written by lane 0 to `flag`, which may be a
+// word of pinned host memory.
 template <typename I>
 __global__ __launch_bounds__(kCheckBlock) void embedding_check_kernel(const I *__restrict__ ids,
                                                                       size_t count, uint64_t rows,
                                                                       uint32_t *__restrict__ flag) {
+    constexpr int kPer = 16 / sizeof(I);
+    // vector part only for a 16-byte aligned id buffer; otherwise all scalar
+    const size_t nvec = ((uintptr_t)ids & 15u) ? 0 : count / kPer;
+    const u32x4 *vecs = reinterpret_cast<const u32x4 *>(ids);
     int bad = 0;
-    for (size_t i = threadIdx.x; i < count; i += kCheckBlock) {
+    for (size_t base = 0; base < nvec; base += (size_t)kCheckBlock * kCheckUnroll) {
+        u32x4 raw[kCheckUnroll];
+#pragma unroll
+        for (int u = 0; u < kCheckUnroll; ++u) {
+            const size_t v = base + threadIdx.x + (size_t)u * kCheckBlock;
+            raw[u] = v < nvec ? vecs[v] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < kCheckUnroll; ++u) {
+            const Vec16<I> ids_vec = __builtin_bit_cast(Vec16<I>, raw[u]);
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) {
+                uint64_t id;
+                bad |= !index_ok(ids_vec.v[e], rows, &id);
+            }
+        }
+    }
+    for (size_t i = nvec * kPer + threadIdx.x; i < count; i += kCheckBlock) {
         uint64_t id;
         bad |= !index_ok(ids[i], rows, &id);
     }
     bad = __syncthreads_or(bad);
-    if (threadIdx.x == 0) *flag = bad ? 1u : 0u;
+    // system scope: visible to the host once the stream has been waited on
+    if (threadIdx.x == 0)
+        __hip_atomic_store(flag, bad ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 template <typename I, bool kThrough>

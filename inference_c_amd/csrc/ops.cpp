@@ -529,23 +529,18 @@ int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *ou
     Staging st("embedding lookup", host, error, capacity);
     if (!st.begin()) return 0;
     if (!host) {
-        ScratchBlock flag(sizeof(uint32_t));
-        uint32_t bad = 1;
-        if (flag.get() == nullptr) {
-            set_error(error, capacity, "embedding lookup: out of device memory");
+        HostWord verdict;
+        if (verdict.get() == nullptr) {
+            set_error(error, capacity, "embedding lookup: cannot allocate pinned host memory");
             return 0;
         }
         if (!hip_ok(k::embedding_check(index_dtype, tensor_buffer_device_handle_internal(indices),
-                                       count, ts[0], static_cast<uint32_t *>(flag.get()),
-                                       st.stream()),
+                                       count, ts[0], verdict.get(), st.stream()),
                     "embedding lookup: index check launch", error, capacity) ||
-            !hip_ok(hipMemcpyAsync(&bad, flag.get(), sizeof bad, hipMemcpyDeviceToHost,
-                                   st.stream()),
-                    "embedding lookup: index check read-back", error, capacity) ||
             !hip_ok(hipStreamSynchronize(st.stream()), "embedding lookup: hipStreamSynchronize",
                     error, capacity))
             return 0;
-        if (bad) {
+        if (verdict.read() != 0) {
             set_error(error, capacity, "%s", bad_index);
             return 0;
         }

@@ -42,6 +42,25 @@ void scratch_clear();
 void *weight_cache_get(const void *host, size_t bytes);
 void weight_cache_clear();
 
+// Words of pinned (page-locked, device-mapped) host memory that a kernel
+// writes and the host reads after waiting for the stream: a verdict without
+// a device-to-host copy. nullptr when none can be allocated.
+uint32_t *host_word_acquire();
+void host_word_release(uint32_t *word);
+
+class HostWord {
+public:
+    HostWord() : word_(host_word_acquire()) {}
+    HostWord(const HostWord &) = delete;
+    HostWord &operator=(const HostWord &) = delete;
+    ~HostWord() { host_word_release(word_); }
+    uint32_t *get() const { return word_; }
+    uint32_t read() const { return *static_cast<volatile uint32_t *>(word_); }
+
+private:
+    uint32_t *word_;
+};
+
 // A pool block held for the duration of one call. Returning it to the pool
 // right after the launches is safe: every later user of the block enqueues
 // on the same SDK stream, after this call's kernels.

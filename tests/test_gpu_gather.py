@@ -78,6 +78,23 @@ def test_rejected_lookup_leaves_output(sdk, orc, device, bad):
     assert_bits_equal(out.download(), before, "output after a rejected call")
 
 
+@pytest.mark.parametrize("index_type", INDEX_TYPES)
+@pytest.mark.parametrize("count,position", [(1, 0), (45, 0), (45, 44), (45, 21),
+                                            (70001, 70000), (70001, 65537)])
+def test_device_index_check_positions(sdk, orc, index_type, count, position):
+    """The device check scans 16-byte vectors of ids, several per lane per
+    step, then a scalar tail: a bad id anywhere is found, a good batch
+    passes."""
+    rows, width = 1000, 8
+    table = sdk.from_numpy(orc.normal((rows, width), 45, 0, 0.0, 1.0, "f16"))
+    ids = ids_for(orc, count, rows, 45).astype(index_type)
+    out = sdk.tensor("f16", (count, width))
+    assert sdk.try_call("tensor_embedding_lookup_f16", table, sdk.from_numpy(ids), out)[0] == 1
+    ids[position] = rows if not np.issubdtype(index_type, np.signedinteger) or position % 2 else -1
+    ok, msg = sdk.try_call("tensor_embedding_lookup_f16", table, sdk.from_numpy(ids), out)
+    assert not ok and msg == "embedding index is negative or outside the table"
+
+
 def test_lookup_mixed_storage_rejected(sdk, orc):
     table = sdk.from_numpy(np.zeros((4, 8), np.float16))
     ids = sdk.from_numpy(np.array([1, 2], np.uint32), device=False)
