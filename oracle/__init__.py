@@ -58,6 +58,9 @@ _SIGS = {
     "orc_view_add_mul_f32": ([_P, _Z, _P, _P, _U64, _P, _P, _P, _P, _P], None),
     "orc_embedding_lookup": ([_P, _Z, _Z, _P, _I, _Z, _P], _I),
     "orc_embedding_gather_u32": ([_P, _Z, _Z, _P, _Z, _P], None),
+    "orc_sdpa_f32": ([_P] * 5 + [_Z] * 7 + [_F, _I, _P], None),
+    "orc_sdpa_f16": ([_P] * 5 + [_Z] * 7 + [_F, _I, _P], None),
+    "orc_sdpa_abs_weight": ([_P] * 5 + [_I] + [_Z] * 7 + [_F, _I, _P], None),
 }
 
 # TensorDType numbering (include/safetensors.h) of numpy index and value types
@@ -279,6 +282,38 @@ class Oracle:
                                            ids.size, out.ctypes.data)
         return out if ok else None
 
+    @staticmethod
+    def _sdpa_dims(q, k, v):
+        batch, qh, ql, dim = q.shape
+        _, kvh, kl, _ = k.shape
+        return batch, qh, kvh, ql, kl, dim, v.shape[3]
+
+    def sdpa(self, q, k, v, mask, scale, causal):
+        """Accelerator-semantics attention (f16 in -> f16 out, f32 -> f32)."""
+        dims = self._sdpa_dims(q, k, v)
+        f16 = q.dtype == np.float16
+        qs, ks, vs = _h(q), _h(k), _h(v)
+        ms = None if mask is None else _h(mask)
+        out = np.empty(dims[:2] + (dims[3], dims[6]), qs.dtype)
+        scratch = np.empty(max(1, dims[4]), np.float32)
+        name = "orc_sdpa_f16" if f16 else "orc_sdpa_f32"
+        getattr(self.lib, name)(qs.ctypes.data, ks.ctypes.data, vs.ctypes.data, _ptr(ms),
+                                out.ctypes.data, *dims, scale, int(causal), scratch.ctypes.data)
+        return out.view(np.float16) if f16 else out
+
+    def sdpa_abs_weight(self, q, k, v, mask, scale, causal):
+        """sum_j p_j |v_j| per output element (f64), the error scale of a
+        reordered accumulation."""
+        dims = self._sdpa_dims(q, k, v)
+        qs, ks, vs = _h(q), _h(k), _h(v)
+        ms = None if mask is None else _h(mask)
+        out = np.empty(dims[:2] + (dims[3], dims[6]), np.float64)
+        scratch = np.empty(max(1, dims[4]), np.float32)
+        self.lib.orc_sdpa_abs_weight(qs.ctypes.data, ks.ctypes.data, vs.ctypes.data, _ptr(ms),
+                                     out.ctypes.data, int(q.dtype == np.float16), *dims, scale,
+                                     int(causal), scratch.ctypes.data)
+        return out
+
     def embedding_gather_u32(self, table, ids):
         """Compute-table slot semantics: uint32 ids, zero rows past the table."""
         t = np.ascontiguousarray(table)
@@ -444,6 +479,27 @@ class Reference:
         finally:
             for h in (ht, hi.value, ho):
                 self.lib.tensor_buffer_free(h)
+
+    def sdpa_f32(self, q, k, v, mask, scale, causal):
+        """tensor_sdpa_f32 of the reference build (its CPU path: no accelerator
+        backend is linked): (ok, out, message)."""
+        hq, hk, hv = self._make("f32", q), self._make("f32", k), self._make("f32", v)
+        hm = None if mask is None else self._make("f32", mask)
+        shape = q.shape[:3] + (v.shape[3],)
+        ho = self._make("f32", np.zeros(shape, np.float32))
+        ws = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(256)
+        assert self.lib.tensor_workspace_create(q.shape[2] * k.shape[2] * 4 + 4096,
+                                                ctypes.byref(ws), err, 256), err.value
+        try:
+            ok = bool(self.lib.tensor_sdpa_f32(hq, hk, hv, hm, scale, int(causal), ho, ws, None,
+                                               err, 256))
+            return ok, self._read(ho, shape, "f32"), err.value.decode()
+        finally:
+            for h in (hq, hk, hv, hm, ho):
+                if h is not None:
+                    self.lib.tensor_buffer_free(h)
+            self.lib.tensor_workspace_free(ws)
 
     def convert(self, array, src, dst):
         h = self._make(src, array)

@@ -646,3 +646,121 @@ void orc_embedding_gather_u32(const void *table, size_t table_rows, size_t row_b
             memset(dst, 0, row_bytes);
     }
 }
+
+/* ---- scaled dot-product attention (accelerator semantics) ---------------- */
+
+/* Follows the accelerator path that tensor_sdpa_f32/f16 take
+   (src/common/attention.c:196-209, :402-429) as the CUDA backend computes it,
+   src/platform/cuda/attention_cuda.cu:25-99:
+     score = (sum_d q[d] k[d], in d order) * scale, + mask[q][k] if a mask is
+             given, and -inf where causal and key > query + (kv_len - q_len);
+     row max over the non-NaN scores; a row whose max is not finite becomes
+             all zeros; otherwise p = expf(s - max), sum in key order,
+             p *= (sum == 0 ? 0 : 1 / sum);
+     out[dv] = sum over keys (in order) of p * v[key][dv].
+   Layouts: q [B, Hq, Lq, D], k [B, Hkv, Lkv, D], v [B, Hkv, Lkv, Dv],
+   mask [Lq, Lkv], out [B, Hq, Lq, Dv]; query head h reads kv head
+   h / (Hq / Hkv). `scores` is caller scratch of Lkv floats. Inputs are read
+   through `load` (f32 or f16 bits), outputs written through `store`. */
+typedef float (*orc_load_fn)(const void *, size_t);
+static float load_f32(const void *p, size_t i) { return ((const float *)p)[i]; }
+static float load_f16(const void *p, size_t i) { return orc_f16_to_f32(((const uint16_t *)p)[i]); }
+
+static void sdpa_generic(const void *q, const void *k, const void *v, const void *mask,
+                         void *out, int f16, size_t batch, size_t qh, size_t kvh, size_t ql,
+                         size_t kl, size_t dim, size_t vdim, float scale, int causal,
+                         float *scores) {
+    const orc_load_fn load = f16 ? load_f16 : load_f32;
+    const size_t group = qh / kvh;
+    const size_t offset = kl > ql ? kl - ql : 0;
+    for (size_t b = 0; b < batch; b++)
+        for (size_t h = 0; h < qh; h++) {
+            const size_t kv = h / group;
+            for (size_t i = 0; i < ql; i++) {
+                const size_t qo = ((b * qh + h) * ql + i) * dim;
+                float maximum = -INFINITY;
+                for (size_t j = 0; j < kl; j++) {
+                    const size_t ko = ((b * kvh + kv) * kl + j) * dim;
+                    float sum = 0.0f;
+                    for (size_t d = 0; d < dim; d++) sum += load(q, qo + d) * load(k, ko + d);
+                    sum *= scale;
+                    if (mask != NULL) sum += load(mask, i * kl + j);
+                    if (causal && j > i + offset) sum = -INFINITY;
+                    scores[j] = sum;
+                    if (sum > maximum) maximum = sum;
+                }
+                const size_t oo = ((b * qh + h) * ql + i) * vdim;
+                if (!isfinite(maximum)) {
+                    for (size_t j = 0; j < kl; j++) scores[j] = 0.0f;
+                } else {
+                    float total = 0.0f;
+                    for (size_t j = 0; j < kl; j++) {
+                        scores[j] = expf(scores[j] - maximum);
+                        total += scores[j];
+                    }
+                    const float inverse = total == 0.0f ? 0.0f : 1.0f / total;
+                    for (size_t j = 0; j < kl; j++) scores[j] *= inverse;
+                }
+                for (size_t e = 0; e < vdim; e++) {
+                    float acc = 0.0f;
+                    for (size_t j = 0; j < kl; j++)
+                        acc += scores[j] * load(v, ((b * kvh + kv) * kl + j) * vdim + e);
+                    if (f16) ((uint16_t *)out)[oo + e] = orc_f32_to_f16(acc);
+                    else ((float *)out)[oo + e] = acc;
+                }
+            }
+        }
+}
+
+void orc_sdpa_f32(const float *q, const float *k, const float *v, const float *mask, float *out,
+                  size_t batch, size_t qh, size_t kvh, size_t ql, size_t kl, size_t dim,
+                  size_t vdim, float scale, int causal, float *scores) {
+    sdpa_generic(q, k, v, mask, out, 0, batch, qh, kvh, ql, kl, dim, vdim, scale, causal, scores);
+}
+
+void orc_sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask,
+                  uint16_t *out, size_t batch, size_t qh, size_t kvh, size_t ql, size_t kl,
+                  size_t dim, size_t vdim, float scale, int causal, float *scores) {
+    sdpa_generic(q, k, v, mask, out, 1, batch, qh, kvh, ql, kl, dim, vdim, scale, causal, scores);
+}
+
+/* Per output element, sum over keys of p * |v| (same p as above), the scale
+   against which a reordered accumulation's error is bounded. Written as f64. */
+void orc_sdpa_abs_weight(const void *q, const void *k, const void *v, const void *mask,
+                         double *out, int f16, size_t batch, size_t qh, size_t kvh, size_t ql,
+                         size_t kl, size_t dim, size_t vdim, float scale, int causal,
+                         float *scores) {
+    const orc_load_fn load = f16 ? load_f16 : load_f32;
+    const size_t group = qh / kvh;
+    const size_t offset = kl > ql ? kl - ql : 0;
+    for (size_t b = 0; b < batch; b++)
+        for (size_t h = 0; h < qh; h++) {
+            const size_t kv = h / group;
+            for (size_t i = 0; i < ql; i++) {
+                const size_t qo = ((b * qh + h) * ql + i) * dim;
+                float maximum = -INFINITY;
+                for (size_t j = 0; j < kl; j++) {
+                    const size_t ko = ((b * kvh + kv) * kl + j) * dim;
+                    float sum = 0.0f;
+                    for (size_t d = 0; d < dim; d++) sum += load(q, qo + d) * load(k, ko + d);
+                    sum *= scale;
+                    if (mask != NULL) sum += load(mask, i * kl + j);
+                    if (causal && j > i + offset) sum = -INFINITY;
+                    scores[j] = sum;
+                    if (sum > maximum) maximum = sum;
+                }
+                double total = 0.0;
+                if (isfinite(maximum))
+                    for (size_t j = 0; j < kl; j++) total += exp((double)scores[j] - maximum);
+                const size_t oo = ((b * qh + h) * ql + i) * vdim;
+                for (size_t e = 0; e < vdim; e++) {
+                    double acc = 0.0;
+                    if (isfinite(maximum) && total > 0.0)
+                        for (size_t j = 0; j < kl; j++)
+                            acc += exp((double)scores[j] - maximum) / total *
+                                   fabs((double)load(v, ((b * kvh + kv) * kl + j) * vdim + e));
+                    out[oo + e] = acc;
+                }
+            }
+        }
+}

@@ -133,6 +133,20 @@ int orc_embedding_lookup(const void *table, size_t table_rows, size_t row_bytes,
 void orc_embedding_gather_u32(const void *table, size_t table_rows, size_t row_bytes,
                               const uint32_t *ids, size_t count, void *out);
 
+/* scaled dot-product attention with the accelerator backend's semantics
+   (q [B,Hq,Lq,D], k [B,Hkv,Lkv,D], v [B,Hkv,Lkv,Dv], mask [Lq,Lkv] or NULL,
+   out [B,Hq,Lq,Dv]); scores = caller scratch of Lkv floats */
+void orc_sdpa_f32(const float *q, const float *k, const float *v, const float *mask, float *out,
+                  size_t batch, size_t qh, size_t kvh, size_t ql, size_t kl, size_t dim,
+                  size_t vdim, float scale, int causal, float *scores);
+void orc_sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask,
+                  uint16_t *out, size_t batch, size_t qh, size_t kvh, size_t ql, size_t kl,
+                  size_t dim, size_t vdim, float scale, int causal, float *scores);
+void orc_sdpa_abs_weight(const void *q, const void *k, const void *v, const void *mask,
+                         double *out, int f16, size_t batch, size_t qh, size_t kvh, size_t ql,
+                         size_t kl, size_t dim, size_t vdim, float scale, int causal,
+                         float *scores);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,3 +133,24 @@ def test_embedding_compute_slot_f32(orc):
     table = np.arange(8, dtype=np.float32).reshape(4, 2)
     got = orc.embedding_gather_u32(table, np.array([2, 0], np.uint32))
     assert got.ravel().tolist() == [4, 5, 0, 1]
+
+
+def test_sdpa_accelerator_semantics_known_answers(orc):
+    # test_attention.c:441-496: the same values whichever backend runs them
+    q = np.array([1, 0, 0, 1, 1, 0, 0, 1], np.float32).reshape(1, 2, 2, 2)
+    k = np.array([1, 0, 0, 1], np.float32).reshape(1, 1, 2, 2)
+    v = np.array([1, 0, 0, 2], np.float32).reshape(1, 1, 2, 2)
+    near = lambda a, b: np.allclose(a, b, atol=1e-5, rtol=0)
+    out = orc.sdpa(q, k, v, None, 1.0, False).ravel()
+    assert near(out[:4], [0.73105858, 0.53788284, 0.26894143, 1.4621172]) and near(out[4:], out[:4])
+    out = orc.sdpa(q, k, v, None, 1.0, True).ravel()
+    assert near(out[:4], [1.0, 0.0, 0.26894143, 1.4621172])
+    mask = np.array([-np.inf, 0, 0, 0], np.float32).reshape(2, 2)
+    out = orc.sdpa(q, k, v, mask, 1.0, False).ravel()
+    assert near(out[:2], [0.0, 2.0])
+    all_masked = np.full((2, 2), -np.inf, np.float32)
+    assert (orc.sdpa(q, k, v, all_masked, 1.0, False) == 0).all()
+    # the same through f16 inputs and outputs
+    out16 = orc.sdpa(q.astype(F16), k.astype(F16), v.astype(F16), None, 1.0, False).ravel()
+    assert np.allclose(out16.astype(np.float32)[:4], [0.73105858, 0.53788284, 0.26894143, 1.4621172],
+                       atol=1e-3, rtol=0)

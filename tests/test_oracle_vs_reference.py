@@ -111,3 +111,49 @@ def test_embedding_lookup_f16_rejects_float_indices(orc, ref):
     ok, _, message = ref.embedding_lookup(table, ids)
     assert not ok and message == "embedding index is negative or outside the table"
     assert orc.embedding_lookup(table, ids) is None
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 2, 5, 9, 16, 8), (2, 2, 1, 33, 33, 64, 64),
+                                   (1, 3, 3, 7, 4, 5, 3), (1, 2, 2, 1, 50, 32, 32)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("masked", [False, True])
+def test_sdpa_f32_matches_reference_cpu_path(orc, ref, shape, causal, masked):
+    """The accelerator-semantics restatement (attention_cuda.cu:25-99) against
+    the reference build's tensor_sdpa_f32 (its CPU loop, attention.c:227-410)
+    on finite inputs: the two differ only in p / sum versus p * (1 / sum), so
+    every output is within a few f32 roundings of sum_j p_j |v_j|."""
+    b, h, kh, lq, lk, d, dv = shape
+    q = orc.normal((b, h, lq, d), 19, 0, 0.0, 1.0, "f32")
+    k = orc.normal((b, kh, lk, d), 19, 1, 0.0, 1.0, "f32")
+    v = orc.normal((b, kh, lk, dv), 19, 2, 0.0, 1.0, "f32")
+    mask = None
+    if masked:
+        mask = orc.uniform((lq, lk), 19, 3, -4.0, 0.0, "f32")
+        mask[:, 0] = -np.inf  # a masked key in every row
+    ok, want, message = ref.sdpa_f32(q, k, v, mask, 0.25, causal)
+    assert ok, message
+    got = orc.sdpa(q, k, v, mask, 0.25, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, mask, 0.25, causal)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert (err <= 1e-6 * weight + 1e-30).all(), float((err / np.maximum(weight, 1e-30)).max())
+
+
+def test_sdpa_special_rows(orc):
+    """Closed forms of the accelerator rules (attention_cuda.cu:44-54): a row
+    whose scores are all -inf is zero; a +inf score makes the row's max
+    non-finite, so the row is zero (the CPU loop would share the row among the
+    +inf keys instead); a NaN score never becomes the max, so a row of only
+    NaN scores is zero, while a NaN beside finite scores makes the row NaN."""
+    q = np.zeros((1, 1, 3, 4), np.float32)
+    q[0, 0, 1] = 1e38           # row 1: scores overflow to +inf
+    q[0, 0, 2] = 1.0            # row 2: finite scores
+    k = np.ones((1, 1, 2, 4), np.float32)
+    k[0, 0, 1, 0] = np.nan       # key 1 scores NaN in every row
+    v = np.arange(4, dtype=np.float32).reshape(1, 1, 2, 2)
+    mask = np.zeros((3, 2), np.float32)
+    mask[0] = -np.inf            # row 0: key 0 masked, key 1 NaN -> no finite max
+    out = orc.sdpa(q, k, v, mask, 1.0, False)
+    assert (out[0, 0, 0] == 0).all() and (out[0, 0, 1] == 0).all()
+    assert np.isnan(out[0, 0, 2]).all()
+    k_all_nan = np.full((1, 1, 2, 4), np.nan, np.float32)
+    assert (orc.sdpa(q, k_all_nan, v, None, 1.0, False) == 0).all()
