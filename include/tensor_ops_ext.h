@@ -205,6 +205,31 @@ int tensor_fill_normal(TensorBuffer *buffer, uint64_t seed, uint64_t stream,
 
 /* ---- stream ------------------------------------------------------------- */
 
+/* ---- attention on device buffers ------------------------------------------ */
+
+/* Scaled dot-product attention on device-storage TensorBuffers, enqueued on
+   the SDK stream: q [B,Hq,Lq,D], k [B,Hkv,Lkv,D], v [B,Hkv,Lkv,Dv],
+   additive_mask [Lq,Lkv] or NULL, output [B,Hq,Lq,Dv]; query head h reads kv
+   head h / (Hq / Hkv); causal masks key j of query i when
+   j > i + (Lkv > Lq ? Lkv - Lq : 0). The arithmetic is the accelerator
+   attention table's (include/attention_backend.h; the reference's CUDA
+   backend, src/platform/cuda/attention_cuda.cu:25-99): a row whose largest
+   score is not finite is all zeros, otherwise softmax(scores) @ v with f32
+   accumulation. Mask values are used as given. D and Dv up to 512.
+   No reference op: the reference's tensor_sdpa_f32/f16
+   (src/common/attention.c:211-431) take host buffers only; shape checks and
+   their messages are the same. */
+int tensor_sdpa_device_f32(const TensorBuffer *query, const TensorBuffer *key,
+                           const TensorBuffer *value,
+                           const TensorBuffer *additive_mask, float scale,
+                           int causal, TensorBuffer *output, char *error,
+                           size_t error_capacity);
+int tensor_sdpa_device_f16(const TensorBuffer *query, const TensorBuffer *key,
+                           const TensorBuffer *value,
+                           const TensorBuffer *additive_mask, float scale,
+                           int causal, TensorBuffer *output, char *error,
+                           size_t error_capacity);
+
 /* The hipStream_t every SDK operation is ordered on (created on first use on
    the current device). Callers may record HIP events on it or make other
    streams wait on it. No reference counterpart (the CUDA backend uses the

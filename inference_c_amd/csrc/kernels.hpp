@@ -106,6 +106,19 @@ hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t
                             size_t row_bytes, size_t elem_bytes, const void *ids, size_t count,
                             void *out, hipStream_t s);
 
+// Scaled dot-product attention with the accelerator semantics of the
+// reference (q [B,Hq,Lq,D], k [B,Hkv,Lkv,D], v [B,Hkv,Lkv,Dv], mask [Lq,Lkv]
+// or null, out [B,Hq,Lq,Dv]). D and Dv up to 512.
+struct SdpaShape {
+    size_t batch, q_heads, kv_heads, q_len, kv_len, head_dim, value_dim;
+};
+hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
+                    float *out, const SdpaShape &shape, float scale, bool causal,
+                    hipStream_t s);
+hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                    const uint16_t *mask, uint16_t *out, const SdpaShape &shape, float scale,
+                    bool causal, hipStream_t s);
+
 // Synthetic inputs (counter-based splitmix64).
 hipError_t fill_uniform(TensorDType dtype, void *y, size_t n, uint64_t seed,
                         uint64_t stream, float low, float high, hipStream_t s);

@@ -56,6 +56,8 @@ OP_ARGTYPES = {
     "tensor_argmax_f32": [_P, _P], "tensor_argmax_f16": [_P, _P],
     "tensor_rope_f32": [_P, _P, _Z, _Z, _Z, _D, _Z], "tensor_rope_f16": [_P, _P, _Z, _Z, _Z, _D, _Z],
     "tensor_fill_uniform": [_P, _U64, _U64, _F, _F], "tensor_fill_normal": [_P, _U64, _U64, _F, _F],
+    "tensor_sdpa_device_f32": [_P, _P, _P, _P, _F, _I, _P],
+    "tensor_sdpa_device_f16": [_P, _P, _P, _P, _F, _I, _P],
     "tensor_device_synchronize": [],
 }
 

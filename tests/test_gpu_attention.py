@@ -1,0 +1,181 @@
+"""Scaled dot-product attention on the GPU against the CPU oracle.
+
+The oracle restates the reference's accelerator semantics
+(src/platform/cuda/attention_cuda.cu:25-99, pinned to the reference build's
+tensor_sdpa_f32 in test_oracle_vs_reference.py). The GPU computes the same
+scores but folds them with an online softmax and normalises once at the end,
+so outputs are compared against sum_j p_j |v_j| (the scale of any reordered
+accumulation of p_j v_j):
+  f32: |got - want| <= 1e-5 * sum_j p_j |v_j|   (north-star f32 reduction bound)
+  f16: within 1 f16 ulp of the oracle, or |got - want| <= 2e-3 * sum_j p_j |v_j|
+       (north-star f16 reduction bound).
+Special rows (all masked, +inf or NaN scores) must match exactly."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.helpers import f16_ulps
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
+    (1, 4, 2, 5, 9, 16, 8),
+    (2, 2, 1, 33, 33, 64, 64),
+    (1, 3, 3, 7, 4, 5, 3),          # dims that are not whole vectors
+    (1, 2, 2, 1, 50, 32, 32),       # a decode step
+    (1, 8, 2, 128, 200, 128, 128),
+    (2, 12, 12, 64, 64, 64, 64),
+    (1, 2, 1, 70, 130, 96, 80),
+    (1, 1, 1, 3, 700, 256, 512),
+]
+
+
+def inputs(orc, shape, dtype, seed, masked):
+    b, h, kh, lq, lk, d, dv = shape
+    q = orc.normal((b, h, lq, d), seed, 0, 0.0, 1.0, dtype)
+    k = orc.normal((b, kh, lk, d), seed, 1, 0.0, 1.0, dtype)
+    v = orc.normal((b, kh, lk, dv), seed, 2, 0.0, 1.0, dtype)
+    mask = None
+    if masked:
+        mask = orc.uniform((lq, lk), seed, 3, -4.0, 0.0, dtype)
+        mask[:, lk // 2] = -np.inf
+    return q, k, v, mask
+
+
+def check(got, want, weight, dtype, what):
+    g = got.astype(np.float64)
+    w = want.astype(np.float64)
+    assert np.array_equal(np.isnan(g), np.isnan(w)), f"{what}: NaN positions differ"
+    g, w, wt = g[~np.isnan(w)], w[~np.isnan(w)], weight[~np.isnan(w)]
+    err = np.abs(g - w)
+    if dtype == "f32":
+        ok = err <= 1e-5 * wt + 1e-30
+    else:
+        ok = (f16_ulps(got[~np.isnan(want.astype(np.float64))],
+                       want[~np.isnan(want.astype(np.float64))]) <= 1) | (err <= 2e-3 * wt)
+    bad = np.flatnonzero(~ok)
+    assert bad.size == 0, (f"{what}: {bad.size} of {ok.size} outside the bound; worst "
+                           f"{float((err / np.maximum(wt, 1e-30)).max()):.3g} of sum p|v|")
+
+
+def run_device(sdk, q, k, v, mask, scale, causal, dtype):
+    tq, tk, tv = sdk.from_numpy(q), sdk.from_numpy(k), sdk.from_numpy(v)
+    tm = None if mask is None else sdk.from_numpy(mask)
+    out = sdk.tensor(dtype, q.shape[:3] + (v.shape[3],))
+    sdk.call(f"tensor_sdpa_device_{dtype}", tq, tk, tv, tm, scale, int(causal), out)
+    return out.download()
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("masked", [False, True])
+def test_device_sdpa(sdk, orc, shape, dtype, causal, masked):
+    q, k, v, mask = inputs(orc, shape, dtype, 30, masked)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, mask, scale, causal, dtype)
+    want = orc.sdpa(q, k, v, mask, scale, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, mask, scale, causal)
+    check(got, want, weight, dtype, f"{shape} causal={causal} mask={masked}")
+
+
+def table_slots(sdk):
+    sdk.lib.tensor_attention_cuda_backend.restype = ctypes.c_void_p
+    return ctypes.cast(sdk.lib.tensor_attention_cuda_backend(), ctypes.POINTER(ctypes.c_void_p))
+
+
+def run_slot(sdk, dtype, q, k, v, mask, scale, causal):
+    slots = table_slots(sdk)
+    P, Z = ctypes.c_void_p, ctypes.c_size_t
+    fn = ctypes.CFUNCTYPE(ctypes.c_int, P, P, P, P, P, Z, Z, Z, Z, Z, Z, Z, ctypes.c_float,
+                          ctypes.c_int)(slots[3] if dtype == "f32" else slots[4])
+    b, h, lq, d = q.shape
+    kh, lk, dv = k.shape[1], k.shape[2], v.shape[3]
+    out = np.zeros((b, h, lq, dv), q.dtype)
+    ok = fn(q.ctypes.data, k.ctypes.data, v.ctypes.data,
+            None if mask is None else mask.ctypes.data, out.ctypes.data, b, h, kh, lq, lk, d, dv,
+            scale, int(causal))
+    return ok, out
+
+
+def test_table_known_answers(sdk):
+    """reference tests/test_attention.c:441-496 through the accelerator
+    table's host-pointer run slot (what tensor_sdpa_f32 calls)."""
+    slots = table_slots(sdk)
+    assert ctypes.CFUNCTYPE(ctypes.c_int)(slots[2])() == 1
+    q = np.array([1, 0, 0, 1, 1, 0, 0, 1], np.float32).reshape(1, 2, 2, 2)
+    k = np.array([1, 0, 0, 1], np.float32).reshape(1, 1, 2, 2)
+    v = np.array([1, 0, 0, 2], np.float32).reshape(1, 1, 2, 2)
+    near = lambda a, b: np.allclose(a, b, atol=1e-5, rtol=0)
+    ok, out = run_slot(sdk, "f32", q, k, v, None, 1.0, False)
+    assert ok and near(out.ravel()[:4], [0.73105858, 0.53788284, 0.26894143, 1.4621172])
+    assert near(out.ravel()[4:], out.ravel()[:4])
+    ok, out = run_slot(sdk, "f32", q, k, v, None, 1.0, True)
+    assert ok and near(out.ravel()[:4], [1.0, 0.0, 0.26894143, 1.4621172])
+    mask = np.array([-np.inf, 0, 0, 0], np.float32).reshape(2, 2)
+    ok, out = run_slot(sdk, "f32", q, k, v, mask, 1.0, False)
+    assert ok and near(out.ravel()[:2], [0.0, 2.0])
+    ok, out = run_slot(sdk, "f32", q, k, v, np.full((2, 2), -np.inf, np.float32), 1.0, False)
+    assert ok and (out == 0).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_table_run_matches_oracle(sdk, orc, dtype):
+    shape = (1, 4, 2, 37, 53, 64, 64)
+    q, k, v, mask = inputs(orc, shape, dtype, 31, True)
+    ok, got = run_slot(sdk, dtype, q, k, v, mask, 0.125, True)
+    assert ok
+    check(got, orc.sdpa(q, k, v, mask, 0.125, True), orc.sdpa_abs_weight(q, k, v, mask, 0.125, True),
+          dtype, "table run")
+
+
+def test_table_rejects_bad_arguments(sdk):
+    q = np.ones((1, 3, 2, 4), np.float32)
+    k = np.ones((1, 2, 2, 4), np.float32)   # 3 query heads over 2 kv heads
+    ok, _ = run_slot(sdk, "f32", q, k, k, None, 1.0, False)
+    assert ok == 0
+    ok, _ = run_slot(sdk, "f32", q[:, :2], k, k, None, float("inf"), False)
+    assert ok == 0
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_special_rows(sdk, orc, dtype):
+    """Rows whose scores are only -inf and NaN are zero; a row whose max is
+    +inf is zero; a NaN score beside finite ones makes the row NaN. Bitwise
+    equal to the oracle, NaN positions included."""
+    npt = np.float16 if dtype == "f16" else np.float32
+    big = 60000.0 if dtype == "f16" else 1e38
+    q = np.zeros((1, 1, 4, 8), npt)
+    q[0, 0, 1] = big           # +inf scores in f32 accumulation
+    q[0, 0, 2] = 1.0
+    q[0, 0, 3] = 0.5
+    k = np.ones((1, 1, 3, 8), npt)
+    k[0, 0, 1, 0] = np.nan
+    v = np.arange(6, dtype=npt).reshape(1, 1, 3, 2)
+    mask = np.zeros((4, 3), npt)
+    mask[0, 0] = mask[0, 2] = -np.inf   # row 0: only the NaN key is left
+    got = run_device(sdk, q, k, v, mask, 1.0, False, dtype)
+    want = orc.sdpa(q, k, v, mask, 1.0, False)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.nan_to_num(got.astype(np.float64)), np.nan_to_num(want.astype(np.float64)))
+    assert (got[0, 0, 0] == 0).all() and np.isnan(got[0, 0, 2]).all()
+    if dtype == "f32":  # 8 * 1e38 overflows the f32 score: max +inf, zero row
+        assert (got[0, 0, 1] == 0).all()
+
+
+def test_device_sdpa_validation(sdk):
+    q = sdk.tensor("f16", (1, 4, 8, 64))
+    k = sdk.tensor("f16", (1, 3, 8, 64))
+    out = sdk.tensor("f16", (1, 4, 8, 64))
+    ok, msg = sdk.try_call("tensor_sdpa_device_f16", q, k, k, None, 1.0, 0, out)
+    assert not ok and msg == "SDPA tensor dimensions do not match"
+    k2 = sdk.tensor("f16", (1, 2, 8, 64))
+    bad_mask = sdk.tensor("f16", (8, 9))
+    ok, msg = sdk.try_call("tensor_sdpa_device_f16", q, k2, k2, bad_mask, 1.0, 0, out)
+    assert not ok and msg == "SDPA mask shape must be [query_length, key_length]"
+    ok, msg = sdk.try_call("tensor_sdpa_device_f16", q, k2, k2, None, 1.0, 2, out)
+    assert not ok and "finite scale" in msg
+    wide = sdk.tensor("f16", (1, 1, 2, 520))
+    ok, msg = sdk.try_call("tensor_sdpa_device_f16", wide, wide, wide, None, 1.0, 0, wide)
+    assert not ok and "up to 512" in msg

@@ -38,6 +38,58 @@ def test_struct_layout_matches_reference_header(tmp_path):
     assert "sizeof TensorComputeBackend 392" in mine
 
 
+def test_attention_table_layout_matches_reference_header(tmp_path):
+    """include/attention_backend.h keeps the reference's
+    src/attention_backend.h layout (the table src/common/attention.c calls)."""
+    ref_src = os.path.join(os.path.dirname(REF_INCLUDE), "src")
+    if not os.path.isdir(ref_src):
+        pytest.skip("reference sources absent")
+    probe = os.path.join(REPO, "oracle", "abi_attention.c")
+
+    def layout(include_dirs, tag):
+        exe = tmp_path / f"attn_{tag}"
+        args = ["gcc", "-std=c11"]
+        for d in include_dirs:
+            args += ["-I", d]
+        subprocess.run(args + ["-o", str(exe), probe], check=True)
+        return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+
+    mine = layout([os.path.join(REPO, "include")], "mine")
+    theirs = layout([ref_src, REF_INCLUDE], "ref")
+    assert mine == theirs
+    assert "TensorAttentionBackendOps.run_f16 32" in mine
+
+
+def test_attention_table_without_device(lib):
+    """The HIP attention table occupies the reference's accelerator slot: its
+    name is "hip", only run/run_f16 are filled, and without a device it
+    reports itself unavailable."""
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    lib.tensor_attention_cuda_backend.restype = ctypes.c_void_p
+    lib.tensor_attention_hip_backend.restype = ctypes.c_void_p
+    table = lib.tensor_attention_cuda_backend()
+    assert table and table == lib.tensor_attention_hip_backend()
+    slots = ctypes.cast(table, ctypes.POINTER(ctypes.c_void_p))
+    assert ctypes.cast(table, ctypes.POINTER(ctypes.c_int))[0] == 2   # TENSOR_ATTENTION_BACKEND_CUDA
+    assert ctypes.cast(slots[1], ctypes.c_char_p).value == b"hip"
+    assert slots[3] and slots[4]                                      # run, run_f16
+    assert not any(slots[i] for i in range(5, 14))                    # decode slots NULL
+    if not sdk.available:
+        assert ctypes.CFUNCTYPE(ctypes.c_int)(slots[2])() == 0
+
+
+def test_device_sdpa_rejects_host_tensors(lib):
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    for dtype in ("f32", "f16"):
+        q = sdk.tensor(dtype, (1, 2, 3, 4), device=False)
+        ok, msg = sdk.try_call(f"tensor_sdpa_device_{dtype}", q, q, q, None, 1.0, 0, q)
+        up = dtype.upper()
+        assert not ok and msg == (f"device SDPA requires rank-4 {up} device tensors, finite "
+                                  f"scale, and optional rank-2 {up} device mask")
+
+
 def test_dtype_helpers(lib):
     sizes = {"UNKNOWN": 0, "BOOL": 1, "U8": 1, "I16": 2, "F16": 2, "BF16": 2, "F32": 4,
              "U32": 4, "F64": 8, "U64": 8}
