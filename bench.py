@@ -31,6 +31,8 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 PEAK_GBPS = 8000.0  # MI355X HBM3E
+# MI355X dense matrix peaks (TFLOP/s): f16 MFMA; f32 MFMA for the f32 path
+MFMA_PEAK_TFLOPS = {"f16": 2500.0, "f32": 157.3}
 
 # Algorithmic bytes and elements per call (each distinct input read once +
 # each output written once).
@@ -293,6 +295,33 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
             lambda s: sdk.call("tensor_embedding_lookup_f16", emb_table, s[0], s[1]),
             2 * tokens * width * 2 + tokens * 4, tokens * width)
     del emb_table
+    # attention (MFMA-bound, not HBM): scaled dot-product attention on device
+    # buffers; flops = 4 * B * Hq * Lq * Lkv * D (half for causal), against
+    # the 2.5 PFLOP/s dense f16 MFMA peak
+    def measure_attention(name, b, hq, hkv, lq, lk, d, causal, dtype="f16"):
+        def make():
+            return (filled(dtype, (b, hq, lq, d), "normal", 7, 0, 0.0, 1.0),
+                    filled(dtype, (b, hkv, lk, d), "normal", 7, 1, 0.0, 1.0),
+                    filled(dtype, (b, hkv, lk, d), "normal", 7, 2, 0.0, 1.0),
+                    T(dtype, (b, hq, lq, d)))
+        flops = 4.0 * b * hq * lq * lk * d * (0.5 if causal else 1.0)
+        size = 2 if dtype == "f16" else 4
+        alg_bytes = (2 * b * hq * lq * d + 2 * b * hkv * lk * d) * size
+        batches, copies = timed(make, lambda s: sdk.call(f"tensor_sdpa_device_{dtype}", s[0], s[1],
+                                                         s[2], None, 1.0 / d ** 0.5, int(causal),
+                                                         s[3]), alg_bytes)
+        best = min(batches)
+        peak = MFMA_PEAK_TFLOPS[dtype]
+        results[name] = {"avg_us": round(best * 1e3, 2),
+                         "batches_us": [round(t * 1e3, 2) for t in batches],
+                         "tflops": round(flops / (best * 1e-3) / 1e12, 1),
+                         "pct_peak_mfma": round(100 * flops / (best * 1e-3) / 1e12 / peak, 1),
+                         "peak_tflops": peak, "flops": flops, "bytes": alg_bytes,
+                         "shape": {"batch": b, "q_heads": hq, "kv_heads": hkv, "q_len": lq,
+                                   "kv_len": lk, "head_dim": d, "causal": causal}}
+    measure_attention("sdpa_f16_prefill_32q8kv_2048_d128_causal", 1, 32, 8, 2048, 2048, 128, True)
+    measure_attention("sdpa_f16_vision_12h_1024_d64", 1, 12, 12, 1024, 1024, 64, False)
+    measure_attention("sdpa_f32_12h_1024_d64", 1, 12, 12, 1024, 1024, 64, False, "f32")
     # cfg5: global sum + max over 2^30 f32 U[-1,1], seed 0
     def cfg5_global():
         return filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0), T("f64", (1,)), T("f32", (1,))

@@ -153,6 +153,240 @@ __global__ __launch_bounds__(kBlock) void sdpa_row_kernel(const S *__restrict__ 
     }
 }
 
+// ---- MFMA flash kernel (f16, D = Dv in {64, 128}) ----------------------------
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// A block owns BM queries of one (batch, head): 32 per wave. Keys come in
+// tiles of 64, staged in LDS by the whole block, double-buffered: the next
+// tile's global loads are issued before the current tile is computed and
+// land in the other buffer afterwards, so one barrier per tile separates the
+// writers of a buffer from its readers. K is stored as [key][dim] rows, V
+// transposed as [dim][slot] with the slot order below.
+//
+// v_mfma_f32_32x32x16_f16 lane layout (checked on the device): A[m][k] in
+// lane l at m = l % 32, k = 8 (l / 32) + i; B[k][n] at n = l % 32,
+// k = 8 (l / 32) + i; D[m][n] at n = l % 32, m = 8 (r / 4) + 4 (l / 32) + r % 4.
+//
+// Scores: S^T = K Q^T per 32-key half tile (A = K rows from LDS, B = the
+// wave's Q rows, loaded once), so lane l holds query l % 32 and, of each
+// half tile, keys 8 (r / 4) + 4 (l / 32) + r % 4; lane l ^ 32 holds the rest.
+// The online softmax runs per lane pair (one swizzle for the max, one for
+// the sum). P^T is then already the B operand of out^T = V^T P^T: chunk c of
+// its k dimension is p[8c .. 8c + 7], keys 16c + 8 (i / 4) + 4 (l / 32) + i % 4,
+// and V^T is stored with that key order (slot 16c + 8h + i), so each A
+// fragment is one 16-byte LDS read.
+constexpr int kFlashN = 64;    // keys per tile
+
+// Block order. MI355X dispatches a launch's workgroups to its 8 XCDs
+// round-robin (block b on XCD b % 8) and each XCD has its own 4 MB L2. The
+// blocks of one (batch, head) read the same K and V tiles, so the grid is
+// renumbered to give each XCD one contiguous range of (head, query block)
+// pairs: a kv head's K/V then live in one L2 instead of being fetched into
+// all eight. (A bijection on [0, n).)
+__device__ inline uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t q = n / kXcds, r = n % kXcds, xcd = b % kXcds, j = b / kXcds;
+    return xcd * q + (xcd < r ? xcd : r) + j;
+}
+
+__device__ inline uint32_t vt_slot(uint32_t key) {
+    const uint32_t within = key % 16;
+    return (key / 16) * 16 + 8 * ((within / 4) % 2) + (within / 8) * 4 + within % 4;
+}
+
+template <int D, int BM, bool kMask>
+__global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__restrict__ q,
+                                                            const _Float16 *__restrict__ k,
+                                                            const _Float16 *__restrict__ v,
+                                                            const _Float16 *__restrict__ mask,
+                                                            _Float16 *__restrict__ out,
+                                                            SdpaArgs a) {
+    constexpr int THREADS = BM * 2;          // one wave per 32 queries
+    constexpr int KC = D / 16;               // 16-dim chunks of Q K^T
+    constexpr int VT = D / 32;               // 32-row tiles of out^T
+    constexpr int KROW = D + 8;              // LDS row of K (halves)
+    constexpr int VROW = kFlashN + 8;        // LDS row of V^T (halves)
+    constexpr int VECS = kFlashN * D / 8;    // 16-byte vectors per K or V tile
+    constexpr int PER = VECS / THREADS;      // per thread, per tile, per operand
+    static_assert(VECS % THREADS == 0, "tile load split");
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashN * KROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[2][D * VROW];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint32_t col = lane & 31, half = lane >> 5;
+    const uint32_t qblocks = (a.ql + BM - 1) / BM;
+    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+    const uint32_t qblock = logical % qblocks;
+    const uint32_t bh = logical / qblocks;
+    const uint32_t head = bh % a.qh, b = bh / a.qh;
+    const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
+    const uint32_t qw = qblock * BM + wave * 32;        // the wave's first query
+    const uint32_t qi = qw + col;                       // the lane's query
+    const bool q_live = qi < a.ql;
+    const float neg_inf = -__builtin_inff();
+
+    half8 qf[KC];
+    {
+        const _Float16 *qrow = q + ((size_t)bh * a.ql + (q_live ? qi : 0)) * D + 8 * half;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) qf[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
+    }
+    float16v o[VT];
+#pragma unroll
+    for (int t = 0; t < VT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+    float m = neg_inf, l = 0.0f;   // running max (log2 units) and sum
+    bool nan_seen = false;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float scale2 = a.scale * kLog2e;
+
+    // keys any query of the block can see, and of this wave
+    const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
+    const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
+                                      : (uint64_t)a.kl;
+    const uint32_t tiles = (uint32_t)((key_end + kFlashN - 1) / kFlashN);
+    const bool wave_live = qw < a.ql;
+    const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
+    const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
+
+    // tile loads: thread `tid` moves vectors tid, tid + THREADS, ... of K
+    // (row-major: key, 8-dim group) and of V (key-fastest, for the transpose)
+    half8 kreg[PER], vreg[PER];
+    auto fetch = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t e = tid + u * THREADS;
+            const uint32_t kk = k0 + e / (D / 8), kc = e % (D / 8);
+            const uint32_t vk = k0 + e % kFlashN, vc = e / kFlashN;
+            kreg[u] = kk < a.kl ? *reinterpret_cast<const half8 *>(k + (kv_base + kk) * D + kc * 8)
+                                : half8{};
+            vreg[u] = vk < a.kl ? *reinterpret_cast<const half8 *>(v + (kv_base + vk) * D + vc * 8)
+                                : half8{};
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t e = tid + u * THREADS;
+            *reinterpret_cast<half8 *>(&ks[buf][(e / (D / 8)) * KROW + (e % (D / 8)) * 8]) = kreg[u];
+            const uint32_t slot = vt_slot(e % kFlashN), vc = e / kFlashN;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vs[buf][(vc * 8 + i) * VROW + slot] = vreg[u][i];
+        }
+    };
+
+    if (tiles > 0) {
+        fetch(0);
+        stash(0);
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        const uint32_t k0 = t * kFlashN;
+        const bool more = t + 1 < tiles;
+        if (more) fetch(k0 + kFlashN);
+        if (wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
+            // interior tile: every key exists and is visible to every query of
+            // the wave, so no per-score bounds or causal test is needed
+            const bool interior = k0 + kFlashN <= a.kl &&
+                                  (!a.causal || (uint64_t)k0 + kFlashN - 1 <= (uint64_t)qw + a.causal_offset);
+            float local_max = neg_inf;
+            // the two 32-key halves are independent accumulation chains:
+            // interleaved, each MFMA's latency is covered by the other's
+            float16v st[2];
+#pragma unroll
+            for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[hblk][r] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c)
+#pragma unroll
+                for (int hblk = 0; hblk < 2; ++hblk) {
+                    const half8 kf = *reinterpret_cast<const half8 *>(
+                        &ks[buf][(32 * hblk + col) * KROW + 16 * c + 8 * half]);
+                    st[hblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], st[hblk], 0, 0, 0);
+                }
+#pragma unroll
+            for (int hblk = 0; hblk < 2; ++hblk) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t kk = k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4;
+                    // scores are kept in log2 units: s * log2(e)
+                    float s = st[hblk][r] * scale2;
+                    if constexpr (kMask) {
+                        if (kk < a.kl && q_live)
+                            s = __builtin_fmaf((float)mask[(size_t)qi * a.kl + kk], kLog2e, s);
+                    }
+                    if (!interior && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
+                        s = neg_inf;
+                    st[hblk][r] = s;
+                    local_max = fmaxf(local_max, s);
+                }
+            }
+            const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
+            const bool none = m_new == neg_inf;   // nothing visible to this query yet
+            if (wave_any(none)) {
+                // a NaN score is dropped while nothing is visible; remember it
+                // (elsewhere it reaches the sum and makes the row NaN itself)
+                bool local_nan = false;
+#pragma unroll
+                for (int r = 0; r < 32; ++r) local_nan = local_nan || st[r / 16][r % 16] != st[r / 16][r % 16];
+                nan_seen = nan_seen || (none && local_nan);
+            }
+            const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+            half8 pf[4];
+            float local_sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                const float p = none ? 0.0f : __builtin_amdgcn_exp2f(st[r / 16][r % 16] - m_new);
+                local_sum += p;
+                pf[r / 8][r % 8] = (_Float16)p;
+            }
+            l = l * alpha + (local_sum + __shfl_xor(local_sum, 32, kWave));
+            m = m_new;
+            const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
+            if (rescale) {
+#pragma unroll
+                for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
+            }
+            // the VT output tiles are independent chains: issue them side by side
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int tt = 0; tt < VT; ++tt) {
+                    const half8 vf = *reinterpret_cast<const half8 *>(
+                        &vs[buf][(32 * tt + col) * VROW + 16 * c + 8 * half]);
+                    o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[tt], 0, 0, 0);
+                }
+        }
+        if (more) stash(buf ^ 1);
+        __syncthreads();
+    }
+    nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
+    if (!q_live) return;
+    const bool zero = !__builtin_isfinite(m);
+    const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
+    const float nan = __builtin_nanf("");
+    _Float16 *orow = out + ((size_t)bh * a.ql + qi) * D;
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            _Float16 quad[4] __attribute__((aligned(8)));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                quad[j] = (_Float16)(zero ? 0.0f : nan_seen ? nan : o[tt][4 * g + j] * inverse);
+            *reinterpret_cast<uint2 *>(orow + 32 * tt + 8 * g + 4 * half) =
+                *reinterpret_cast<const uint2 *>(quad);
+        }
+}
+
 template <typename S>
 hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out,
                        const k::SdpaShape &sh, float scale, bool causal, hipStream_t s) {
@@ -206,6 +440,51 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                     const uint16_t *mask, uint16_t *out, const SdpaShape &shape, float scale,
                     bool causal, hipStream_t s) {
     auto h = [](const uint16_t *p) { return reinterpret_cast<const _Float16 *>(p); };
+    const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
+    const uint64_t lim = 0x7fffffffull;
+    if (aligned && shape.head_dim == shape.value_dim &&
+        (shape.head_dim == 64 || shape.head_dim == 128) && shape.batch && shape.q_heads &&
+        shape.kv_heads && shape.q_heads % shape.kv_heads == 0 && shape.q_len &&
+        shape.q_len <= lim && shape.kv_len && shape.kv_len <= lim &&
+        shape.batch * shape.q_heads * ((shape.q_len + 63) / 64) <= 0x7fffffffull) {
+        SdpaArgs a{};
+        a.batch = (uint32_t)shape.batch;
+        a.qh = (uint32_t)shape.q_heads;
+        a.kvh = (uint32_t)shape.kv_heads;
+        a.group = (uint32_t)(shape.q_heads / shape.kv_heads);
+        a.ql = (uint32_t)shape.q_len;
+        a.kl = (uint32_t)shape.kv_len;
+        a.dim = a.vdim = (uint32_t)shape.head_dim;
+        a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
+        a.scale = scale;
+        a.causal = causal ? 1 : 0;
+        // 128-query blocks (4 waves) when that still gives two blocks per CU,
+        // else 64-query blocks (2 waves) for more of them
+        const size_t bhs = shape.batch * shape.q_heads;
+        const bool wide = ((shape.q_len + 127) / 128) * bhs >= 512;
+        const size_t gx = (shape.q_len + (wide ? 127 : 63)) / (wide ? 128 : 64);
+        const dim3 grid((unsigned)(gx * bhs)), block(wide ? 256 : 128);
+        const _Float16 *m16 = h(mask);
+        _Float16 *o16 = reinterpret_cast<_Float16 *>(out);
+#define ICSDK_FLASH(D, BM)                                                                        \
+    do {                                                                                          \
+        if (mask)                                                                                 \
+            hipLaunchKernelGGL((sdpa_flash_kernel<D, BM, true>), grid, block, 0, s, h(q), h(k),     \
+                               h(v), m16, o16, a);                                                \
+        else                                                                                      \
+            hipLaunchKernelGGL((sdpa_flash_kernel<D, BM, false>), grid, block, 0, s, h(q), h(k),    \
+                               h(v), m16, o16, a);                                                \
+    } while (0)
+        if (shape.head_dim == 64) {
+            if (wide) ICSDK_FLASH(64, 128);
+            else ICSDK_FLASH(64, 64);
+        } else {
+            if (wide) ICSDK_FLASH(128, 128);
+            else ICSDK_FLASH(128, 64);
+        }
+#undef ICSDK_FLASH
+        return hipGetLastError();
+    }
     return launch_sdpa<_Float16>(h(q), h(k), h(v), h(mask), reinterpret_cast<_Float16 *>(out),
                                  shape, scale, causal, s);
 }

@@ -28,6 +28,9 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (2, 12, 12, 64, 64, 64, 64),
     (1, 2, 1, 70, 130, 96, 80),
     (1, 1, 1, 3, 700, 256, 512),
+    (1, 4, 1, 300, 300, 128, 128),  # MFMA path: ragged query and key tiles, 4 heads per kv head
+    (1, 2, 2, 129, 1000, 64, 64),   # MFMA path: kv longer than q (causal offset 871)
+    (3, 2, 2, 1, 77, 128, 128),     # MFMA path: one query
 ]
 
 
