@@ -7,11 +7,12 @@
 // Host-pointer slots are synchronous: operands are staged through the device
 // pool (reused across calls, released by release_cache), the kernel runs on
 // the SDK stream and the outputs are copied back before the slot returns.
-// The embedding slots keep their table uploaded per host address, as the
-// CUDA backend does, until release_cache.
+// The embedding, linear and quantized-linear slots keep their table / weight
+// uploaded per host address, as the CUDA backend does, until release_cache.
 // *_device slots take raw device addresses and only enqueue. Argument checks
 // mirror the CUDA wrappers (non-null pointers, nonzero sizes, no size_t
 // overflow); a failed check returns 0.
+#include "gemm.hpp"
 #include "kernels.hpp"
 #include "sdk.hpp"
 #include "staging.hpp"
@@ -263,9 +264,196 @@ int embedding32(const float *t, const uint32_t *ids, float *o, size_t r, size_t 
     return host_embedding(t, ids, o, r, w, tr);
 }
 
+// ---- GEMM-adjacent slots ----------------------------------------------------
+// CUDA: linear / linear_resident (tensor_compute_cuda.cu:174-214, :399-427),
+// quantized linear (:216-265, :695-713), rms_norm_linear_f32, mlp_f16 and
+// qkv_f16 (:769-786). Dimensions above INT_MAX are refused as cuBLAS does.
+
+template <typename T> constexpr TensorDType dtype_of() {
+    return sizeof(T) == 4 ? TENSOR_DTYPE_F32 : TENSOR_DTYPE_F16;
+}
+
+bool linear_dims_ok(size_t rows, size_t in, size_t out, size_t elem) {
+    constexpr size_t kIntMax = 2147483647;
+    size_t a, b, c;
+    return rows != 0 && in != 0 && out != 0 && rows <= kIntMax && in <= kIntMax &&
+           out <= kIntMax && product(rows, in, &a) && product(out, in, &b) &&
+           product(rows, out, &c) && a <= SIZE_MAX / elem && b <= SIZE_MAX / elem &&
+           c <= SIZE_MAX / elem;
+}
+
+// y[rows][out] = x[rows][in] w[out][in]^T: host pointers, w cached per address
+template <typename T>
+int host_linear(const T *x, const T *w, T *y, size_t rows, size_t in, size_t out) {
+    if (x == nullptr || w == nullptr || y == nullptr || !linear_dims_ok(rows, in, out, sizeof(T)))
+        return 0;
+    Staging st("hip linear", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const void *dw = weight_cache_get(w, out * in * sizeof(T));
+    if (dw == nullptr) return 0;
+    const void *px = st.in(x, rows * in * sizeof(T));
+    void *py = st.out(y, rows * out * sizeof(T));
+    if (st.failed() ||
+        !gemm(GemmKind::kLinear, dtype_of<T>(), px, dw, nullptr, py, rows, in, out, st.stream(),
+              nullptr, 0))
+        return 0;
+    return st.finish(hipSuccess) ? 1 : 0;
+}
+int linear32(const float *x, const float *w, float *y, size_t r, size_t i, size_t o) {
+    return host_linear(x, w, y, r, i, o);
+}
+int linear16(const uint16_t *x, const uint16_t *w, uint16_t *y, size_t r, size_t i, size_t o) {
+    return host_linear(x, w, y, r, i, o);
+}
+
+template <typename T>
+int device_linear(const void *x, const void *w, void *y, size_t rows, size_t in, size_t out) {
+    if (x == nullptr || w == nullptr || y == nullptr || !linear_dims_ok(rows, in, out, sizeof(T)) ||
+        !sdk_ready(nullptr, 0))
+        return 0;
+    return gemm(GemmKind::kLinear, dtype_of<T>(), x, w, nullptr, y, rows, in, out, sdk_stream(),
+                nullptr, 0) ? 1 : 0;
+}
+int linear32_device(const void *x, const void *w, void *y, size_t r, size_t i, size_t o) {
+    return device_linear<float>(x, w, y, r, i, o);
+}
+int linear16_device(const void *x, const void *w, void *y, size_t r, size_t i, size_t o) {
+    return device_linear<uint16_t>(x, w, y, r, i, o);
+}
+
+bool quant_dims_ok(bool q8, size_t rows, size_t in, size_t out) {
+    size_t a, b;
+    return rows != 0 && in != 0 && out != 0 && in % 32 == 0 && product(rows, in, &a) &&
+           product(rows, out, &b) && a <= SIZE_MAX / 2 && b <= SIZE_MAX / 2 &&
+           out <= SIZE_MAX / (in / 32) / (q8 ? 34u : 18u);
+}
+
+hipError_t quant_launch(bool q8, const void *x, const void *w, void *y, size_t rows, size_t in,
+                        size_t out, hipStream_t s) {
+    auto *hx = static_cast<const uint16_t *>(x);
+    auto *pw = static_cast<const uint8_t *>(w);
+    auto *hy = static_cast<uint16_t *>(y);
+    return q8 ? k::linear_q8_0_f16(hx, pw, hy, rows, in, out, s)
+              : k::linear_q4_0_f16(hx, pw, hy, rows, in, out, s);
+}
+
+int quant_device(bool q8, const void *x, const void *w, void *y, size_t rows, size_t in,
+                 size_t out) {
+    if (x == nullptr || w == nullptr || y == nullptr || !quant_dims_ok(q8, rows, in, out) ||
+        !sdk_ready(nullptr, 0))
+        return 0;
+    return quant_launch(q8, x, w, y, rows, in, out, sdk_stream()) == hipSuccess;
+}
+int q8_device(const void *x, const void *w, void *y, size_t r, size_t i, size_t o) {
+    return quant_device(true, x, w, y, r, i, o);
+}
+int q4_device(const void *x, const void *w, void *y, size_t r, size_t i, size_t o) {
+    return quant_device(false, x, w, y, r, i, o);
+}
+
+int quant_host(bool q8, const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+               size_t in, size_t out) {
+    if (x == nullptr || w == nullptr || y == nullptr || !quant_dims_ok(q8, rows, in, out))
+        return 0;
+    Staging st("hip quantized linear", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const void *dw = weight_cache_get(w, out * (in / 32) * (q8 ? 34u : 18u));
+    if (dw == nullptr) return 0;
+    const void *px = st.in(x, rows * in * sizeof(uint16_t));
+    void *py = st.out(y, rows * out * sizeof(uint16_t));
+    if (st.failed()) return 0;
+    return st.finish(quant_launch(q8, px, dw, py, rows, in, out, st.stream())) ? 1 : 0;
+}
+int q8_host(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t r, size_t i, size_t o) {
+    return quant_host(true, x, w, y, r, i, o);
+}
+int q4_host(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t r, size_t i, size_t o) {
+    return quant_host(false, x, w, y, r, i, o);
+}
+
+// norm = RMSNorm(x) * scale, y = norm w^T; both outputs written back
+int rms_linear32(const float *x, const float *scale, float *norm, const float *w, float *y,
+                 size_t rows, size_t in, size_t out, float eps) {
+    if (x == nullptr || scale == nullptr || norm == nullptr || w == nullptr || y == nullptr ||
+        !linear_dims_ok(rows, in, out, sizeof(float)))
+        return 0;
+    Staging st("hip rms_norm_linear", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const void *dw = weight_cache_get(w, out * in * sizeof(float));
+    if (dw == nullptr) return 0;
+    const void *px = st.in(x, rows * in * sizeof(float));
+    const void *ps = st.in(scale, in * sizeof(float));
+    void *pn = st.out(norm, rows * in * sizeof(float));
+    void *py = st.out(y, rows * out * sizeof(float));
+    if (st.failed()) return 0;
+    const hipError_t status =
+        k::rms_norm_f32(static_cast<const float *>(px), static_cast<const float *>(ps),
+                        static_cast<float *>(pn), rows, in, eps, st.stream());
+    if (status != hipSuccess ||
+        !gemm(GemmKind::kLinear, TENSOR_DTYPE_F32, pn, dw, nullptr, py, rows, in, out,
+              st.stream(), nullptr, 0))
+        return 0;
+    return st.finish(hipSuccess) ? 1 : 0;
+}
+
+// y = (gelu(x w1^T + b1)) w2^T + b2 (CUDA: linear, bias+GELU, linear, bias)
+int mlp16(const uint16_t *x, const uint16_t *w1, const uint16_t *b1, const uint16_t *w2,
+          const uint16_t *b2, uint16_t *y, size_t rows, size_t in, size_t mid, size_t out) {
+    if (x == nullptr || w1 == nullptr || b1 == nullptr || w2 == nullptr || b2 == nullptr ||
+        y == nullptr || !linear_dims_ok(rows, in, mid, 2) || !linear_dims_ok(rows, mid, out, 2))
+        return 0;
+    Staging st("hip mlp", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const void *dw1 = weight_cache_get(w1, mid * in * 2);
+    const void *dw2 = weight_cache_get(w2, out * mid * 2);
+    if (dw1 == nullptr || dw2 == nullptr) return 0;
+    const void *px = st.in(x, rows * in * 2);
+    const void *pb1 = st.in(b1, mid * 2);
+    const void *pb2 = st.in(b2, out * 2);
+    void *py = st.out(y, rows * out * 2);
+    ScratchBlock raw(rows * mid * 2), act(rows * mid * 2);
+    if (st.failed() || raw.get() == nullptr || act.get() == nullptr) return 0;
+    auto *hraw = static_cast<uint16_t *>(raw.get());
+    auto *hact = static_cast<uint16_t *>(act.get());
+    if (!gemm(GemmKind::kLinear, TENSOR_DTYPE_F16, px, dw1, nullptr, hraw, rows, in, mid,
+              st.stream(), nullptr, 0) ||
+        k::bias_add_f16(hraw, static_cast<const uint16_t *>(pb1), hact, rows, mid, true,
+                        st.stream()) != hipSuccess ||
+        !gemm(GemmKind::kLinear, TENSOR_DTYPE_F16, hact, dw2, pb2, py, rows, mid, out,
+              st.stream(), nullptr, 0))
+        return 0;
+    return st.finish(hipSuccess) ? 1 : 0;
+}
+
+// q/k/v = x w^T (+ bias); biases optional
+int qkv16(const uint16_t *x, const uint16_t *wq, const uint16_t *wk, const uint16_t *wv,
+          const uint16_t *bq, const uint16_t *bk, const uint16_t *bv, uint16_t *q, uint16_t *k,
+          uint16_t *v, size_t rows, size_t in, size_t out) {
+    if (x == nullptr || wq == nullptr || wk == nullptr || wv == nullptr || q == nullptr ||
+        k == nullptr || v == nullptr || !linear_dims_ok(rows, in, out, 2))
+        return 0;
+    Staging st("hip qkv", true, nullptr, 0);
+    if (!st.begin()) return 0;
+    const uint16_t *weights[3] = {wq, wk, wv};
+    const uint16_t *biases[3] = {bq, bk, bv};
+    uint16_t *outs[3] = {q, k, v};
+    const void *px = st.in(x, rows * in * 2);
+    for (int i = 0; i < 3; ++i) {
+        const void *dw = weight_cache_get(weights[i], out * in * 2);
+        const void *pb = biases[i] ? st.in(biases[i], out * 2) : nullptr;
+        void *py = st.out(outs[i], rows * out * 2);
+        if (dw == nullptr || st.failed() ||
+            !gemm(GemmKind::kLinear, TENSOR_DTYPE_F16, px, dw, pb, py, rows, in, out,
+                  st.stream(), nullptr, 0))
+            return 0;
+    }
+    return st.finish(hipSuccess) ? 1 : 0;
+}
+
 void release_cache(void) {
     scratch_clear();
     weight_cache_clear();
+    gemm_release();
 }
 
 // Device-resident slots: raw device addresses, enqueue only.
@@ -324,6 +512,17 @@ extern "C" const TensorComputeBackend *tensor_compute_hip_backend(void) {
         b.argmax_f32 = argmax32;
         b.embedding_f32 = embedding32;
         b.release_cache = release_cache;
+        b.linear_f32 = linear32;
+        b.linear_f16 = linear16;
+        b.linear_f32_device = linear32_device;
+        b.linear_f16_device = linear16_device;
+        b.linear_q8_0_f16_device = q8_device;
+        b.linear_q4_0_f16_device = q4_device;
+        b.linear_q8_0_f16 = q8_host;
+        b.linear_q4_0_f16 = q4_host;
+        b.rms_norm_linear_f32 = rms_linear32;
+        b.mlp_f16 = mlp16;
+        b.qkv_f16 = qkv16;
         b.bias_add_f32_device = bias32_device;
         b.bias_add_f16_device = bias16_device;
         b.residual_add_f16_device = residual16_device;

@@ -1,0 +1,347 @@
+// Q8_0 / Q4_0 weights: the quantizer and the quantized linear (GEMV) kernels.
+//
+// Packed layout (reference src/common/tensor_quant.c:48-100): an [out, in]
+// f16 matrix becomes [out, in/32, block] bytes; each 32-weight block is a
+// little-endian f16 scale followed by 32 int8 values (Q8_0, 34 bytes) or by
+// 16 bytes holding weight j in the low nibble and weight j+16 in the high
+// nibble of byte j, stored as value + 8 (Q4_0, 18 bytes).
+//
+// quant_gemv_kernel: y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
+// A wave owns O output rows; its 64 lanes walk the blocks of those rows
+// (lane l takes blocks l, l+64, ...), so the wave reads each weight row as
+// one contiguous stream. A block starts on a 2-byte boundary: the lane loads
+// the 4-byte words covering it and re-aligns them with v_perm_b32. The int8 /
+// nibble values are turned into exact f16 pairs (0x6400 | byte is 1024 +
+// byte; one packed f16 subtract removes the offset) and multiplied with the
+// x pairs by v_dot2_f32_f16, f32 accumulation. x for the lane's block is
+// loaded once and reused for all O rows. The wave's partial sums are folded
+// with DPP at the end. Bound: HBM bytes of the packed weights (1.0625 or
+// 0.5625 bytes per weight) for small row counts.
+#include "kern_common.hpp"
+#include "kernels.hpp"
+
+namespace icsdk {
+namespace k {
+namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+template <bool kQ8> struct Fmt {
+    static constexpr uint32_t kBytes = kQ8 ? 34 : 18;
+    static constexpr int kWords = kQ8 ? 8 : 4;  // 4-byte words of packed values
+};
+
+__device__ inline half2_t as_half2(uint32_t bits) { return __builtin_bit_cast(half2_t, bits); }
+
+// Loads the block at byte address `addr` (2-byte aligned): its scale and its
+// packed values re-aligned to 4-byte words. Every access stays inside the
+// block or the 2 bytes before it, which share its aligned 4-byte word.
+template <bool kQ8>
+__device__ inline float load_block(const uint8_t *addr, uint32_t (&q)[Fmt<kQ8>::kWords]) {
+    constexpr int W = Fmt<kQ8>::kWords;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(addr);
+    const bool shifted = (a & 2) != 0;
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    uint32_t e[W + 1];
+#pragma unroll
+    for (int i = 0; i < W; ++i) e[i] = __builtin_nontemporal_load(words + i);
+    // word W: its low half is the block's last two bytes when the block is
+    // aligned; a shifted block ends with the whole word
+    const uint16_t *tail = reinterpret_cast<const uint16_t *>(words + W);
+    uint32_t last = tail[0];
+    if (shifted) last |= uint32_t(tail[1]) << 16;
+    e[W] = last;
+    const uint32_t sel = shifted ? 0x07060504u : 0x05040302u;
+#pragma unroll
+    for (int i = 0; i < W; ++i) q[i] = __builtin_amdgcn_perm(e[i + 1], e[i], sel);
+    const uint32_t scale_bits = shifted ? (e[0] >> 16) : (e[0] & 0xffffu);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)scale_bits);
+}
+
+// sum_k x_k q_k of one block in f32; x holds the block's 32 f16 as 16 pairs.
+template <bool kQ8>
+__device__ inline float block_dot(const uint32_t (&q)[Fmt<kQ8>::kWords], const uint32_t (&x)[16]) {
+    const half2_t bias8 = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
+    const half2_t bias4 = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
+    float s0 = 0.0f, s1 = 0.0f;
+    if constexpr (kQ8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // int8 -> offset binary, two bytes per f16 pair
+            const uint32_t u = q[j] ^ 0x80808080u;
+            const half2_t lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias8;
+            const half2_t hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias8;
+            s0 = __builtin_amdgcn_fdot2(lo, as_half2(x[2 * j]), s0, false);
+            s1 = __builtin_amdgcn_fdot2(hi, as_half2(x[2 * j + 1]), s1, false);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // bytes 4j, 4j+1 and 4j+2, 4j+3 spread to the low byte of each half
+            const uint32_t p01 = __builtin_amdgcn_perm(0u, q[j], 0x0c010c00u);
+            const uint32_t p23 = __builtin_amdgcn_perm(0u, q[j], 0x0c030c02u);
+            const half2_t w01 = as_half2((p01 & 0x000f000fu) | 0x64006400u) - bias4;
+            const half2_t w23 = as_half2((p23 & 0x000f000fu) | 0x64006400u) - bias4;
+            const half2_t w1617 = as_half2(((p01 >> 4) & 0x000f000fu) | 0x64006400u) - bias4;
+            const half2_t w1819 = as_half2(((p23 >> 4) & 0x000f000fu) | 0x64006400u) - bias4;
+            s0 = __builtin_amdgcn_fdot2(w01, as_half2(x[2 * j]), s0, false);
+            s1 = __builtin_amdgcn_fdot2(w23, as_half2(x[2 * j + 1]), s1, false);
+            s0 = __builtin_amdgcn_fdot2(w1617, as_half2(x[8 + 2 * j]), s0, false);
+            s1 = __builtin_amdgcn_fdot2(w1819, as_half2(x[8 + 2 * j + 1]), s1, false);
+        }
+    }
+    return s0 + s1;
+}
+
+// Grid: x = waves of O output rows (4 waves per block), y = groups of R input
+// rows. Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
+template <bool kQ8, int R, int O>
+__global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__restrict__ x,
+                                                            const uint8_t *__restrict__ w,
+                                                            uint16_t *__restrict__ y,
+                                                            uint32_t rows, uint32_t in,
+                                                            uint32_t out) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(
+        (blockIdx.x * kBlock + threadIdx.x) / kWave);
+    const uint32_t o0 = wave * O;
+    if (o0 >= out) return;
+    const uint32_t r0 = blockIdx.y * R;
+    const uint32_t blocks = in / 32;
+    const uint64_t row_bytes = (uint64_t)blocks * Fmt<kQ8>::kBytes;
+    // rows past the end are clamped onto the last one (computed, not stored)
+    uint32_t orow[O], xrow[R];
+#pragma unroll
+    for (int o = 0; o < O; ++o) orow[o] = min(o0 + o, out - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) xrow[r] = min(r0 + r, rows - 1);
+
+    float acc[O][R];
+#pragma unroll
+    for (int o = 0; o < O; ++o)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[o][r] = 0.0f;
+
+    for (uint32_t b = lane; b < blocks; b += kWave) {
+        uint32_t q[O][Fmt<kQ8>::kWords];
+        float scale[O];
+#pragma unroll
+        for (int o = 0; o < O; ++o)
+            scale[o] = load_block<kQ8>(w + orow[o] * row_bytes + (uint64_t)b * Fmt<kQ8>::kBytes, q[o]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4 *xp = reinterpret_cast<const u32x4 *>(x + (uint64_t)xrow[r] * in + b * 32);
+            uint32_t xv[16];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const u32x4 t = xp[v];
+                xv[4 * v] = t.x;
+                xv[4 * v + 1] = t.y;
+                xv[4 * v + 2] = t.z;
+                xv[4 * v + 3] = t.w;
+            }
+#pragma unroll
+            for (int o = 0; o < O; ++o)
+                acc[o][r] = __builtin_fmaf(scale[o], block_dot<kQ8>(q[o], xv), acc[o][r]);
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < O; ++o)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float total = wave_sum(acc[o][r]);
+            if (lane == 0 && o0 + o < out && r0 + r < rows)
+                y[(uint64_t)(r0 + r) * out + o0 + o] =
+                    __builtin_bit_cast(uint16_t, (_Float16)total);
+        }
+}
+
+// Any alignment: one thread per output, bytes read one at a time.
+template <bool kQ8>
+__global__ __launch_bounds__(kBlock) void quant_linear_scalar_kernel(const uint16_t *__restrict__ x,
+                                                                     const uint8_t *__restrict__ w,
+                                                                     uint16_t *__restrict__ y,
+                                                                     uint64_t rows, uint32_t in,
+                                                                     uint32_t out) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= rows * out) return;
+    const uint64_t r = i / out, o = i % out;
+    const uint32_t blocks = in / 32;
+    const uint8_t *base = w + o * blocks * Fmt<kQ8>::kBytes;
+    float sum = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) {
+        const uint8_t *blk = base + (uint64_t)b * Fmt<kQ8>::kBytes;
+        const float scale = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8)));
+        float part = 0.0f;
+        for (uint32_t k = 0; k < 32; ++k) {
+            int v;
+            if constexpr (kQ8) {
+                v = (int)(int8_t)blk[2 + k];
+            } else {
+                const uint8_t packed = blk[2 + (k & 15)];
+                v = (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
+            }
+            const float xv = (float)__builtin_bit_cast(_Float16, x[r * in + b * 32 + k]);
+            part = __builtin_fmaf(xv, (float)v, part);
+        }
+        sum = __builtin_fmaf(scale, part, sum);
+    }
+    y[i] = __builtin_bit_cast(uint16_t, (_Float16)sum);
+}
+
+// The quantizer's scale rounding (src/common/tensor_quant.c:28-46): round to
+// nearest even in the normal range. Below 2^-14 the reference shifts one
+// place short of binary16, storing round-half-up(v * 2^25) -- twice the
+// subnormal value -- and that is the packed format, so it is kept; magnitudes
+// under 2^-25 become signed zero.
+__device__ inline uint16_t quant_scale_bits(float value) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int exponent = (int)((bits >> 23) & 255u) - 127 + 15;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent <= 0) {
+        if (exponent < -10) return (uint16_t)sign;
+        mantissa |= 0x800000u;
+        const int shift = 13 - exponent;
+        return (uint16_t)(sign | ((mantissa + (1u << (shift - 1))) >> shift));
+    }
+    if (exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+    mantissa += 0xfffu + ((mantissa >> 13) & 1u);
+    if (mantissa & 0x800000u) return (uint16_t)(sign | (uint32_t)(exponent + 1) << 10);
+    return (uint16_t)(sign | (uint32_t)exponent << 10 | (mantissa >> 13));
+}
+
+// One thread per 32-weight block; the arithmetic is the reference's, with
+// every product, sum and quotient rounded on its own (no contraction).
+// A non-finite weight sets *bad.
+template <bool kQ8>
+__global__ __launch_bounds__(kBlock) void quantize_kernel(const uint16_t *__restrict__ weight,
+                                                          uint8_t *__restrict__ packed,
+                                                          uint32_t *__restrict__ bad,
+                                                          uint64_t total_blocks) {
+    const uint64_t t = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= total_blocks) return;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(weight + t * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const Vec16<_Float16> h = __builtin_bit_cast(Vec16<_Float16>, src[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[8 * i + j] = (float)h.v[j];
+    }
+    float max_abs = 0.0f, max_signed = 0.0f;
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        finite = finite && __builtin_isfinite(v[j]);
+        if (__builtin_fabsf(v[j]) > max_abs) max_abs = __builtin_fabsf(v[j]);
+        if (__builtin_fabsf(v[j]) > __builtin_fabsf(max_signed)) max_signed = v[j];
+    }
+    if (!finite) __hip_atomic_store(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float scale = kQ8 ? __fdiv_rn(max_abs, 127.0f) : __fdiv_rn(max_signed, -8.0f);
+    const float inverse = scale == 0.0f ? 0.0f : __fdiv_rn(1.0f, scale);
+    uint16_t *dst = reinterpret_cast<uint16_t *>(packed + t * Fmt<kQ8>::kBytes);
+    dst[0] = quant_scale_bits(scale);
+    if constexpr (kQ8) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int lo = (int)__builtin_rintf(__fmul_rn(v[2 * j], inverse));
+            int hi = (int)__builtin_rintf(__fmul_rn(v[2 * j + 1], inverse));
+            lo = min(max(lo, -127), 127);
+            hi = min(max(hi, -127), 127);
+            dst[1 + j] = (uint16_t)((uint32_t)(uint8_t)(int8_t)lo | (uint32_t)(uint8_t)(int8_t)hi << 8);
+        }
+    } else {
+        uint32_t bytes[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int lo = (int)__fadd_rn(__fmul_rn(v[j], inverse), 8.5f);
+            int hi = (int)__fadd_rn(__fmul_rn(v[j + 16], inverse), 8.5f);
+            lo = min(max(lo, 0), 15);
+            hi = min(max(hi, 0), 15);
+            bytes[j] = (uint32_t)(lo | (hi << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[1 + j] = (uint16_t)(bytes[2 * j] | bytes[2 * j + 1] << 8);
+    }
+}
+
+template <bool kQ8, int R, int O>
+hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                       size_t in, size_t out, hipStream_t s) {
+    constexpr uint32_t kWavesPerBlock = kBlock / kWave;
+    const size_t waves = (out + O - 1) / O;
+    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock),
+                    (unsigned)((rows + R - 1) / R));
+    quant_gemv_kernel<kQ8, R, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                         (uint32_t)out);
+    return hipGetLastError();
+}
+
+template <bool kQ8>
+hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                        size_t in, size_t out, hipStream_t s) {
+    const bool vector_path = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                             reinterpret_cast<uintptr_t>(w) % 4 == 0 && in <= 0xffffffffu &&
+                             out <= 0xffffffffu;
+    if (!vector_path) {
+        const size_t n = rows * out;
+        const size_t blocks = (n + kBlock - 1) / kBlock;
+        if (blocks > 0x7fffffffu || in > 0xffffffffu || out > 0xffffffffu) return hipErrorInvalidValue;
+        quant_linear_scalar_kernel<kQ8><<<(unsigned)blocks, kBlock, 0, s>>>(x, w, y, rows,
+                                                                              (uint32_t)in,
+                                                                              (uint32_t)out);
+        return hipGetLastError();
+    }
+    // row groups per launch stay within the grid's y limit
+    constexpr size_t kMaxGroups = 65535;
+    for (size_t r0 = 0; r0 < rows;) {
+        const size_t left = rows - r0;
+        const uint16_t *xr = x + r0 * in;
+        uint16_t *yr = y + r0 * out;
+        hipError_t status;
+        size_t done;
+        if (left <= 1) {
+            status = launch_gemv<kQ8, 1, 2>(xr, w, yr, left, in, out, s);
+            done = left;
+        } else if (left <= 2) {
+            status = launch_gemv<kQ8, 2, 2>(xr, w, yr, left, in, out, s);
+            done = left;
+        } else if (left <= 4) {
+            status = launch_gemv<kQ8, 4, 1>(xr, w, yr, left, in, out, s);
+            done = left;
+        } else {
+            done = left < kMaxGroups * 8 ? left : kMaxGroups * 8;
+            status = launch_gemv<kQ8, 8, 1>(xr, w, yr, done, in, out, s);
+        }
+        if (status != hipSuccess) return status;
+        r0 += done;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t linear_q8_0_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                           size_t in, size_t out, hipStream_t s) {
+    return linear_quant<true>(x, w, y, rows, in, out, s);
+}
+
+hipError_t linear_q4_0_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                           size_t in, size_t out, hipStream_t s) {
+    return linear_quant<false>(x, w, y, rows, in, out, s);
+}
+
+hipError_t quantize_f16(bool q8, const uint16_t *weight, uint8_t *packed, uint32_t *bad,
+                        size_t total_blocks, hipStream_t s) {
+    const size_t blocks = (total_blocks + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    if (q8)
+        quantize_kernel<true><<<(unsigned)blocks, kBlock, 0, s>>>(weight, packed, bad, total_blocks);
+    else
+        quantize_kernel<false><<<(unsigned)blocks, kBlock, 0, s>>>(weight, packed, bad, total_blocks);
+    return hipGetLastError();
+}
+
+}  // namespace k
+}  // namespace icsdk

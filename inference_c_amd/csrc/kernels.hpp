@@ -119,6 +119,17 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                     const uint16_t *mask, uint16_t *out, const SdpaShape &shape, float scale,
                     bool causal, hipStream_t s);
 
+// Quantized linear y[rows, out] = x[rows, in] * dequant(w)^T with w packed
+// [out, in/32, 34] (Q8_0) or [out, in/32, 18] (Q4_0); in % 32 == 0.
+hipError_t linear_q8_0_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                           size_t in, size_t out, hipStream_t s);
+hipError_t linear_q4_0_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                           size_t in, size_t out, hipStream_t s);
+// Packs total_blocks 32-weight f16 blocks (16-byte aligned) into Q8_0 / Q4_0
+// blocks; a non-finite weight sets *bad to 1.
+hipError_t quantize_f16(bool q8, const uint16_t *weight, uint8_t *packed, uint32_t *bad,
+                        size_t total_blocks, hipStream_t s);
+
 // Synthetic inputs (counter-based splitmix64).
 hipError_t fill_uniform(TensorDType dtype, void *y, size_t n, uint64_t seed,
                         uint64_t stream, float low, float high, hipStream_t s);

@@ -555,31 +555,12 @@ int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *ou
     return st.finish(status) ? 1 : 0;
 }
 
-int out_of_scope(const char *op, char *error, size_t capacity) {
-    set_error(error, capacity,
-              "%s is not provided by the HIP tensor-ops library (GEMM work is outside its "
-              "scope)", op);
-    return 0;
-}
-
 }  // namespace
 
 extern "C" {
 
 // ---- include/tensor_ops.h ------------------------------------------------
 
-int tensor_matmul_f32(Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_matmul_f32", error, capacity);
-}
-int tensor_matmul_f16(Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_matmul_f16", error, capacity);
-}
-int tensor_linear_f32(Buf, Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_linear_f32", error, capacity);
-}
-int tensor_linear_f16(Buf, Buf, Buf, TensorBuffer *, char *error, size_t capacity) {
-    return out_of_scope("tensor_linear_f16", error, capacity);
-}
 int tensor_embedding_lookup_f32(Buf table, Buf indices, TensorBuffer *output, char *error,
                                 size_t capacity) {
     return embedding_lookup(TENSOR_DTYPE_F32, table, indices, output, error, capacity);

@@ -58,6 +58,7 @@ OP_ARGTYPES = {
     "tensor_fill_uniform": [_P, _U64, _U64, _F, _F], "tensor_fill_normal": [_P, _U64, _U64, _F, _F],
     "tensor_sdpa_device_f32": [_P, _P, _P, _P, _F, _I, _P],
     "tensor_sdpa_device_f16": [_P, _P, _P, _P, _F, _I, _P],
+    "tensor_linear_q8_0_f16": [_P, _P, _P], "tensor_linear_q4_0_f16": [_P, _P, _P],
     "tensor_device_synchronize": [],
 }
 
@@ -130,6 +131,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tensor_dtype_size.restype = _Z
     lib.tensor_dtype_name.argtypes = [_I]
     lib.tensor_dtype_name.restype = ctypes.c_char_p
+    lib.tensor_quantize_linear_weight_f16.argtypes = [_P, _Z, _Z, _I, ctypes.POINTER(_P),
+                                                      ctypes.c_char_p, _Z]
+    lib.tensor_quantize_linear_weight_f16.restype = _I
     return lib
 
 
@@ -235,6 +239,25 @@ class Sdk:
         if isinstance(a, ctypes.Structure):
             return ctypes.addressof(a)
         return a
+
+    def quantize(self, weight: np.ndarray, fmt: int) -> tuple[int, Optional[np.ndarray], str]:
+        """tensor_quantize_linear_weight_f16 on an f16 [out, in] matrix
+        (fmt 1 = Q8_0, 2 = Q4_0): (ok, packed uint8 [out, in/32, block], message)."""
+        w = np.ascontiguousarray(weight, np.float16)
+        result = _P()
+        err = ctypes.create_string_buffer(512)
+        ok = self.lib.tensor_quantize_linear_weight_f16(w.ctypes.data, w.shape[0], w.shape[1], fmt,
+                                                        ctypes.byref(result), err, 512)
+        if not ok:
+            return 0, None, err.value.decode()
+        try:
+            shape = ctypes.cast(self.lib.tensor_buffer_shape(result),
+                                ctypes.POINTER(ctypes.c_uint64))
+            packed = np.empty((shape[0], shape[1], shape[2]), np.uint8)
+            ctypes.memmove(packed.ctypes.data, self.lib.tensor_buffer_data(result), packed.nbytes)
+            return 1, packed, ""
+        finally:
+            self.lib.tensor_buffer_free(result)
 
     def synchronize(self) -> None:
         self.call("tensor_device_synchronize")

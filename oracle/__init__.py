@@ -61,7 +61,18 @@ _SIGS = {
     "orc_sdpa_f32": ([_P] * 5 + [_Z] * 7 + [_F, _I, _P], None),
     "orc_sdpa_f16": ([_P] * 5 + [_Z] * 7 + [_F, _I, _P], None),
     "orc_sdpa_abs_weight": ([_P] * 5 + [_I] + [_Z] * 7 + [_F, _I, _P], None),
+    "orc_matmul_f32": ([_P, _P, _P, _Z, _Z, _Z], None),
+    "orc_matmul_f16": ([_P, _P, _P, _Z, _Z, _Z], None),
+    "orc_linear_f32": ([_P, _P, _P, _P, _Z, _Z, _Z], None),
+    "orc_linear_f16": ([_P, _P, _P, _P, _Z, _Z, _Z], None),
+    "orc_quant_scale_to_f16": ([_F], _U16),
+    "orc_quantize_f16": ([_P, _Z, _Z, _I, _P], _I),
+    "orc_linear_quant_f16": ([_P, _P, _P, _Z, _Z, _Z, _I], None),
+    "orc_linear_quant_abs_weight": ([_P, _P, _P, _Z, _Z, _Z, _I], None),
 }
+
+# bytes per 32-weight block of each TensorWeightQuantization format
+QUANT_BLOCK_BYTES = {1: 34, 2: 18}
 
 # TensorDType numbering (include/safetensors.h) of numpy index and value types
 INDEX_DTYPES = {np.dtype(np.int16): 4, np.dtype(np.uint16): 5, np.dtype(np.int32): 6,
@@ -314,6 +325,53 @@ class Oracle:
                                      int(causal), scratch.ctypes.data)
         return out
 
+    def matmul(self, a, b):
+        """tensor_matmul_* host loop: [rows, inner] x [inner, cols]."""
+        f16 = a.dtype == np.float16
+        out = np.empty((a.shape[0], b.shape[1]), np.uint16 if f16 else np.float32)
+        name = "orc_matmul_f16" if f16 else "orc_matmul_f32"
+        getattr(self.lib, name)(_h(a).ctypes.data, _h(b).ctypes.data, out.ctypes.data,
+                                a.shape[0], a.shape[1], b.shape[1])
+        return out.view(np.float16) if f16 else out
+
+    def linear(self, x, w, bias=None):
+        """tensor_linear_* host loop: x [..., in] times w [out, in]^T plus bias."""
+        f16 = x.dtype == np.float16
+        rows = int(np.prod(x.shape[:-1]))
+        out = np.empty(x.shape[:-1] + (w.shape[0],), np.uint16 if f16 else np.float32)
+        name = "orc_linear_f16" if f16 else "orc_linear_f32"
+        getattr(self.lib, name)(_h(x).ctypes.data, _h(w).ctypes.data,
+                                None if bias is None else _h(bias).ctypes.data, out.ctypes.data,
+                                rows, w.shape[1], w.shape[0])
+        return out.view(np.float16) if f16 else out
+
+    def quantize(self, w, fmt):
+        """tensor_quantize_linear_weight_f16: packed uint8 [out, in/32, block]
+        for an f16 [out, in] matrix, or None when refused."""
+        out, inw = w.shape
+        if inw % 32:
+            return None
+        packed = np.zeros((out, inw // 32, QUANT_BLOCK_BYTES[fmt]), np.uint8)
+        ok = self.lib.orc_quantize_f16(_h(w).ctypes.data, out, inw, fmt, packed.ctypes.data)
+        return packed if ok else None
+
+    def linear_quant(self, x, packed, q8):
+        """The CUDA backend's quantized linear: f16 x [..., in], packed
+        weights [out, in/32, block] -> f16 [..., out]."""
+        rows, inw = int(np.prod(x.shape[:-1])), x.shape[-1]
+        out = np.empty(x.shape[:-1] + (packed.shape[0],), np.uint16)
+        self.lib.orc_linear_quant_f16(_h(x).ctypes.data, np.ascontiguousarray(packed).ctypes.data,
+                                      out.ctypes.data, rows, inw, packed.shape[0], int(q8))
+        return out.view(np.float16)
+
+    def linear_quant_abs_weight(self, x, packed, q8):
+        rows, inw = int(np.prod(x.shape[:-1])), x.shape[-1]
+        out = np.empty(x.shape[:-1] + (packed.shape[0],), np.float64)
+        self.lib.orc_linear_quant_abs_weight(_h(x).ctypes.data,
+                                             np.ascontiguousarray(packed).ctypes.data,
+                                             out.ctypes.data, rows, inw, packed.shape[0], int(q8))
+        return out
+
     def embedding_gather_u32(self, table, ids):
         """Compute-table slot semantics: uint32 ids, zero rows past the table."""
         t = np.ascontiguousarray(table)
@@ -358,8 +416,15 @@ class Reference:
         for name in ("tensor_silu_f32", "tensor_silu_f16"):
             getattr(lib, name).argtypes = [_P, _P, ctypes.c_char_p, _Z]
         lib.tensor_residual_add_f16.argtypes = [_P, _P, _P, ctypes.c_char_p, _Z]
-        for name in ("tensor_embedding_lookup_f32", "tensor_embedding_lookup_f16"):
+        for name in ("tensor_embedding_lookup_f32", "tensor_embedding_lookup_f16",
+                     "tensor_matmul_f32", "tensor_matmul_f16"):
             getattr(lib, name).argtypes = [_P, _P, _P, ctypes.c_char_p, _Z]
+        for name in ("tensor_linear_f32", "tensor_linear_f16"):
+            getattr(lib, name).argtypes = [_P, _P, _P, _P, ctypes.c_char_p, _Z]
+        lib.tensor_quantize_linear_weight_f16.argtypes = [_P, _Z, _Z, _I, ctypes.POINTER(_P),
+                                                          ctypes.c_char_p, _Z]
+        lib.tensor_buffer_shape.argtypes = [_P]
+        lib.tensor_buffer_shape.restype = ctypes.POINTER(_U64)
         self.lib = lib
 
     def _make(self, dtype, array):
@@ -500,6 +565,47 @@ class Reference:
                 if h is not None:
                     self.lib.tensor_buffer_free(h)
             self.lib.tensor_workspace_free(ws)
+
+    def _call(self, name, operands, out_shape, dtype):
+        """Runs a tensor_ops entry point on host buffers: (ok, out, message)."""
+        handles = [None if a is None else self._make(dtype, a) for a in operands]
+        ho = self._make(dtype, np.zeros(out_shape, np.float16 if dtype == "f16" else np.float32))
+        err = ctypes.create_string_buffer(256)
+        try:
+            ok = bool(getattr(self.lib, name)(*handles, ho, err, 256))
+            return ok, self._read(ho, out_shape, dtype), err.value.decode()
+        finally:
+            for h in handles + [ho]:
+                if h is not None:
+                    self.lib.tensor_buffer_free(h)
+
+    def matmul(self, a, b):
+        dtype = "f16" if a.dtype == np.float16 else "f32"
+        return self._call(f"tensor_matmul_{dtype}", [a, b], (a.shape[0], b.shape[1]), dtype)
+
+    def linear(self, x, w, bias=None):
+        dtype = "f16" if x.dtype == np.float16 else "f32"
+        return self._call(f"tensor_linear_{dtype}", [x, w, bias], x.shape[:-1] + (w.shape[0],),
+                          dtype)
+
+    def quantize(self, w, fmt):
+        """tensor_quantize_linear_weight_f16: (ok, packed uint8 or None, message)."""
+        bits = _h(np.ascontiguousarray(w, np.float16))
+        result = _P()
+        err = ctypes.create_string_buffer(256)
+        ok = bool(self.lib.tensor_quantize_linear_weight_f16(bits.ctypes.data, w.shape[0],
+                                                              w.shape[1], fmt,
+                                                              ctypes.byref(result), err, 256))
+        if not ok:
+            return False, None, err.value.decode()
+        try:
+            shape = self.lib.tensor_buffer_shape(result)
+            dims = (shape[0], shape[1], shape[2])
+            packed = np.empty(dims, np.uint8)
+            ctypes.memmove(packed.ctypes.data, self.lib.tensor_buffer_data_mut(result), packed.nbytes)
+            return True, packed, ""
+        finally:
+            self.lib.tensor_buffer_free(result)
 
     def convert(self, array, src, dst):
         h = self._make(src, array)

@@ -764,3 +764,178 @@ void orc_sdpa_abs_weight(const void *q, const void *k, const void *v, const void
             }
         }
 }
+
+/* ---- matmul / linear (src/common/tensor_ops.c:163-398) ------------------ */
+
+/* tensor_ops.c:163-193 (f32) and :195-215 (f16 through f32): one float sum
+   per output, started at 0, over the inner index in order. */
+void orc_matmul_f32(const float *a, const float *b, float *y, size_t rows, size_t inner,
+                    size_t cols) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < inner; k++) sum += a[r * inner + k] * b[k * cols + c];
+            y[r * cols + c] = sum;
+        }
+}
+
+void orc_matmul_f16(const uint16_t *a, const uint16_t *b, uint16_t *y, size_t rows,
+                    size_t inner, size_t cols) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < inner; k++)
+                sum += orc_f16_to_f32(a[r * inner + k]) * orc_f16_to_f32(b[k * cols + c]);
+            y[r * cols + c] = orc_f32_to_f16(sum);
+        }
+}
+
+/* Host path of tensor_linear_f32 (tensor_ops.c:290-307) and _f16 (:389-396):
+   y[r][o] = bias[o] (or 0) + sum_i x[r][i] * w[o][i], one float sum in input
+   order; f16 rounds once at the end. */
+void orc_linear_f32(const float *x, const float *w, const float *bias, float *y, size_t rows,
+                    size_t in, size_t out) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t o = 0; o < out; o++) {
+            float sum = bias == NULL ? 0.0f : bias[o];
+            for (size_t i = 0; i < in; i++) sum += x[r * in + i] * w[o * in + i];
+            y[r * out + o] = sum;
+        }
+}
+
+void orc_linear_f16(const uint16_t *x, const uint16_t *w, const uint16_t *bias, uint16_t *y,
+                    size_t rows, size_t in, size_t out) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t o = 0; o < out; o++) {
+            float sum = bias == NULL ? 0.0f : orc_f16_to_f32(bias[o]);
+            for (size_t i = 0; i < in; i++)
+                sum += orc_f16_to_f32(x[r * in + i]) * orc_f16_to_f32(w[o * in + i]);
+            y[r * out + o] = orc_f32_to_f16(sum);
+        }
+}
+
+/* ---- Q8_0 / Q4_0 weights (src/common/tensor_quant.c) --------------------- */
+
+/* The quantizer's own scale rounding (tensor_quant.c:28-46): round to nearest
+   even for normal halves. Below 2^-14 the reference adds half of the dropped
+   range and shifts by 13 - e instead of 14 - e, so the stored bits are
+   round-half-up(v * 2^25): twice the subnormal value v would round to.
+   Magnitudes under 2^-25 become signed zero. Kept as the reference has it:
+   the packed bytes are its format. */
+static uint16_t quant_scale_to_f16(float value) {
+    const uint32_t bits = bits_of(value);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const int exponent = (int)((bits >> 23) & 255u) - 127 + 15;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent <= 0) {
+        if (exponent < -10) return sign;
+        mantissa |= 0x800000u;
+        const int shift = 13 + -exponent;
+        return (uint16_t)(sign | ((mantissa + (1u << (shift - 1))) >> shift));
+    }
+    if (exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+    mantissa += 0xfffu + ((mantissa >> 13) & 1u);
+    if (mantissa & 0x800000u) return (uint16_t)(sign | (uint16_t)((exponent + 1) << 10));
+    return (uint16_t)(sign | (uint16_t)(exponent << 10) | (uint16_t)(mantissa >> 13));
+}
+
+uint16_t orc_quant_scale_to_f16(float value) { return quant_scale_to_f16(value); }
+
+/* tensor_quantize_linear_weight_f16 (tensor_quant.c:48-100) into `dst`
+   ([out, in/32, 34 or 18] bytes). Per 32-weight block: Q8_0 stores
+   scale = max|x| / 127 and q = clamp(lrintf(x / scale), -127, 127) as int8;
+   Q4_0 stores scale = x* / -8 (x* the first element of largest magnitude)
+   and q = clamp((int)(x / scale + 8.5), 0, 15) packed two per byte (element
+   j low nibble, j + 16 high nibble). Returns 0 (dst partly written) on a
+   non-finite weight or unsupported arguments. */
+int orc_quantize_f16(const uint16_t *weight, size_t out, size_t in, int format, uint8_t *dst) {
+    const size_t block_bytes = format == 1 ? 34 : format == 2 ? 18 : 0;
+    if (weight == NULL || out == 0 || in == 0 || in % 32 || block_bytes == 0) return 0;
+    const size_t blocks = in / 32;
+    for (size_t row = 0; row < out; row++)
+        for (size_t b = 0; b < blocks; b++) {
+            float x[32], max_abs = 0.0f, max_signed = 0.0f;
+            for (size_t j = 0; j < 32; j++) {
+                x[j] = orc_f16_to_f32(weight[row * in + b * 32 + j]);
+                if (!isfinite(x[j])) return 0;
+                if (fabsf(x[j]) > max_abs) max_abs = fabsf(x[j]);
+                if (fabsf(x[j]) > fabsf(max_signed)) max_signed = x[j];
+            }
+            uint8_t *block = dst + (row * blocks + b) * block_bytes;
+            const float scale = format == 1 ? max_abs / 127.0f : max_signed / -8.0f;
+            const uint16_t half = quant_scale_to_f16(scale);
+            block[0] = (uint8_t)half;
+            block[1] = (uint8_t)(half >> 8);
+            const float inverse = scale == 0.0f ? 0.0f : 1.0f / scale;
+            if (format == 1) {
+                for (size_t j = 0; j < 32; j++) {
+                    long q = lrintf(x[j] * inverse);
+                    if (q < -127) q = -127;
+                    if (q > 127) q = 127;
+                    block[2 + j] = (uint8_t)(int8_t)q;
+                }
+            } else {
+                for (size_t j = 0; j < 16; j++) {
+                    int lo = (int)(x[j] * inverse + 8.5f);
+                    int hi = (int)(x[j + 16] * inverse + 8.5f);
+                    lo = lo < 0 ? 0 : lo > 15 ? 15 : lo;
+                    hi = hi < 0 ? 0 : hi > 15 ? 15 : hi;
+                    block[2 + j] = (uint8_t)(lo | (hi << 4));
+                }
+            }
+        }
+    return 1;
+}
+
+/* Weight k (0..31) of a packed block: int8 for Q8_0, nibble - 8 for Q4_0
+   (src/platform/cuda/tensor_compute_cuda.cu:230-233). */
+static int quant_value(const uint8_t *block, int q8, size_t k) {
+    if (q8) return (int)(int8_t)block[2 + k];
+    const uint8_t packed = block[2 + (k & 15)];
+    return (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
+}
+
+static float quant_scale(const uint8_t *block) {
+    return orc_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+}
+
+/* The CUDA backend's quantized linear (tensor_compute_cuda.cu:216-238):
+   y[r][o] = f16(sum over blocks b, then k of fmaf(x[r][32b+k], scale_b * q,
+   sum)), one float sum per output started at 0. */
+void orc_linear_quant_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                          size_t in, size_t out, int q8) {
+    const size_t blocks = in / 32, block_bytes = q8 ? 34 : 18;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t o = 0; o < out; o++) {
+            const uint8_t *base = w + o * blocks * block_bytes;
+            float sum = 0.0f;
+            for (size_t b = 0; b < blocks; b++) {
+                const uint8_t *block = base + b * block_bytes;
+                const float scale = quant_scale(block);
+                for (size_t k = 0; k < 32; k++)
+                    sum = fmaf(orc_f16_to_f32(x[r * in + b * 32 + k]),
+                               scale * (float)quant_value(block, q8, k), sum);
+            }
+            y[r * out + o] = orc_f32_to_f16(sum);
+        }
+}
+
+/* sum over k of |x[r][k] * scale * q| in double: the error scale of any
+   reordered accumulation of the products above. */
+void orc_linear_quant_abs_weight(const uint16_t *x, const uint8_t *w, double *y, size_t rows,
+                                 size_t in, size_t out, int q8) {
+    const size_t blocks = in / 32, block_bytes = q8 ? 34 : 18;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t o = 0; o < out; o++) {
+            const uint8_t *base = w + o * blocks * block_bytes;
+            double sum = 0.0;
+            for (size_t b = 0; b < blocks; b++) {
+                const uint8_t *block = base + b * block_bytes;
+                const double scale = quant_scale(block);
+                for (size_t k = 0; k < 32; k++)
+                    sum += fabs((double)orc_f16_to_f32(x[r * in + b * 32 + k]) * scale *
+                                (double)quant_value(block, q8, k));
+            }
+            y[r * out + o] = sum;
+        }
+}

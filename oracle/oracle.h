@@ -22,6 +22,17 @@
  *   row/global reduce  closed form vs numpy float64
  *   rope               known answers + norm preservation + position 0 identity
  *   view add/mul       brute-force index math on tiny shapes (numpy)
+ *   embedding lookup   known answers + accept/reject and rows bit-exact vs
+ *                      oracle/_ref for every index dtype + numpy.take
+ *   sdpa               known answers + vs oracle/_ref tensor_sdpa_f32 within
+ *                      a few roundings of sum p|v| + special-row closed forms
+ *   matmul / linear    bit-exact vs oracle/_ref tensor_matmul_* /
+ *                      tensor_linear_* (host path) + known answers
+ *   quantize           bit-exact vs oracle/_ref
+ *                      tensor_quantize_linear_weight_f16 + known answers
+ *   quantized linear   known answer (the reference test's own check) + a
+ *                      double-precision dot product of the dequantized
+ *                      weights within the f32 rounding bound
  */
 #ifndef INFERENCE_ORACLE_H
 #define INFERENCE_ORACLE_H
@@ -146,6 +157,25 @@ void orc_sdpa_abs_weight(const void *q, const void *k, const void *v, const void
                          double *out, int f16, size_t batch, size_t qh, size_t kvh, size_t ql,
                          size_t kl, size_t dim, size_t vdim, float scale, int causal,
                          float *scores);
+
+/* matmul y[rows,cols] = a[rows,inner] b[inner,cols]; linear y[rows,out] =
+   x[rows,in] w[out,in]^T (+ bias[out]) -- the reference's host loops */
+void orc_matmul_f32(const float *a, const float *b, float *y, size_t rows, size_t inner,
+                    size_t cols);
+void orc_matmul_f16(const uint16_t *a, const uint16_t *b, uint16_t *y, size_t rows,
+                    size_t inner, size_t cols);
+void orc_linear_f32(const float *x, const float *w, const float *bias, float *y, size_t rows,
+                    size_t in, size_t out);
+void orc_linear_f16(const uint16_t *x, const uint16_t *w, const uint16_t *bias, uint16_t *y,
+                    size_t rows, size_t in, size_t out);
+
+/* Q8_0 (format 1, 34-byte blocks) / Q4_0 (format 2, 18-byte blocks) */
+uint16_t orc_quant_scale_to_f16(float value);
+int orc_quantize_f16(const uint16_t *weight, size_t out, size_t in, int format, uint8_t *dst);
+void orc_linear_quant_f16(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
+                          size_t in, size_t out, int q8);
+void orc_linear_quant_abs_weight(const uint16_t *x, const uint8_t *w, double *y, size_t rows,
+                                 size_t in, size_t out, int q8);
 
 #ifdef __cplusplus
 }

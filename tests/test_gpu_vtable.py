@@ -66,9 +66,14 @@ def test_table_shape(hip):
     t = hip["table"]
     assert ctypes.cast(t.name, ctypes.c_char_p).value == b"hip"
     assert ctypes.CFUNCTYPE(I)(t.is_available)() == 1
-    for slot in ("linear_f32", "linear_f16", "mlp_f16", "qkv_f16", "vision_layer_f16",
-                 "linear_f16_device", "rms_norm_linear_f32"):
-        assert getattr(t, slot) is None, f"{slot} should be NULL (GEMM, outside this library)"
+    for slot in ("linear_f32", "linear_f16", "mlp_f16", "qkv_f16", "linear_f32_device",
+                 "linear_f16_device", "rms_norm_linear_f32", "linear_q8_0_f16_device",
+                 "linear_q4_0_f16_device", "linear_q8_0_f16", "linear_q4_0_f16"):
+        assert getattr(t, slot), f"{slot} is NULL"
+    # whole transformer layers (model harness code) are not provided
+    for slot in ("mlp_f32", "vision_layer_f16", "vision_layer_f32", "vision_sequence_begin_f16",
+                 "vision_sequence_layer_quant_f16", "vision_sequence_begin_f32"):
+        assert getattr(t, slot) is None, f"{slot} should be NULL"
     assert t.release_cache
 
 

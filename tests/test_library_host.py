@@ -129,19 +129,74 @@ def test_host_tensor_buffer_contract(lib):
         sdk.tensor("f32", (1 << 40, 1 << 40), device=False)
 
 
-def test_out_of_scope_entry_points_fail_with_a_message(lib):
-    from inference_c_amd import Sdk
-    sdk = Sdk()
-    a = sdk.tensor("f32", (2, 2), device=False)
-    for name in ("tensor_matmul_f32", "tensor_matmul_f16"):
-        ok, msg = sdk.try_call(name, a, a, a)
-        assert not ok and "not provided by the HIP tensor-ops library" in msg
-    ok, msg = sdk.try_call("tensor_linear_f16", a, a, None, a)
-    assert not ok and "not provided by the HIP tensor-ops library" in msg
+def test_tensor_store_entry_points_fail_with_a_message(lib):
     err = ctypes.create_string_buffer(256)
     res = ctypes.c_void_p(1)
     assert not lib.tensor_buffer_load(None, b"w", ctypes.byref(res), err, 256)
     assert res.value is None and b"tensor stores are not part of" in err.value
+
+
+def test_linear_and_matmul_validation_matches_reference(lib, ref, orc):
+    """tensor_matmul_* / tensor_linear_* refuse bad host operands with the
+    reference's messages (src/common/tensor_ops.c:163-398) before any device
+    work, and an empty batch succeeds without one."""
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    f32 = lambda *shape: np.zeros(shape, np.float32)
+    f16 = lambda *shape: np.zeros(shape, np.float16)
+    cases = [
+        ("tensor_matmul_f32", [f32(2, 3), f32(3, 2)], f32(4)),
+        ("tensor_matmul_f32", [f32(2, 3), f32(4, 2)], f32(2, 2)),
+        ("tensor_matmul_f16", [f16(2, 3), f16(3, 5)], f16(2, 4)),
+        ("tensor_linear_f32", [f32(2, 3), f32(3), None], f32(2, 3)),
+        ("tensor_linear_f32", [f32(2, 3), f32(4, 3), f32(5)], f32(2, 4)),
+        ("tensor_linear_f16", [f16(2, 3), f16(4, 2), None], f16(2, 4)),
+        ("tensor_linear_f16", [f16(2, 5, 3), f16(4, 3), None], f16(2, 4, 4)),
+        ("tensor_linear_f32", [f32(2, 3), f32(4, 3), f32(4, 1)], f32(2, 4)),
+        ("tensor_linear_f32", [f32(2, 0), f32(4, 0), None], f32(2, 4)),
+    ]
+    for name, operands, out in cases:
+        dtype = "f16" if out.dtype == np.float16 else "f32"
+        rok, _, rmsg = ref._call(name, operands, out.shape, dtype)
+        args = [None if a is None else sdk.from_numpy(a, device=False) for a in operands]
+        ok, msg = sdk.try_call(name, *args, sdk.from_numpy(out, device=False))
+        assert not rok and not ok and msg == rmsg, (name, msg, rmsg)
+    # mixed dtypes within one call
+    ok, msg = sdk.try_call("tensor_matmul_f32", sdk.from_numpy(f32(2, 2), device=False),
+                           sdk.from_numpy(f16(2, 2), device=False),
+                           sdk.from_numpy(f32(2, 2), device=False))
+    assert not ok and msg == "matmul requires rank-2 F32 tensors"
+    # empty batches: nothing to compute, success with or without a device
+    ok, _ = sdk.try_call("tensor_linear_f32", sdk.from_numpy(f32(0, 3), device=False),
+                         sdk.from_numpy(f32(4, 3), device=False), None,
+                         sdk.from_numpy(f32(0, 4), device=False))
+    assert ok
+    ok, _ = sdk.try_call("tensor_matmul_f16", sdk.from_numpy(f16(0, 3), device=False),
+                         sdk.from_numpy(f16(3, 2), device=False),
+                         sdk.from_numpy(f16(0, 2), device=False))
+    assert ok
+    if not sdk.available:
+        ok, msg = sdk.try_call("tensor_matmul_f32", sdk.from_numpy(f32(2, 3), device=False),
+                               sdk.from_numpy(f32(3, 2), device=False),
+                               sdk.from_numpy(f32(2, 2), device=False))
+        assert not ok and msg.startswith("HIP device unavailable")
+
+
+def test_quantize_refusals_match_reference(lib, ref):
+    """tensor_quantize_linear_weight_f16 argument checks (tensor_quant.c:
+    48-60): the same message, no result, before any device work."""
+    from inference_c_amd import Sdk
+    sdk = Sdk()
+    message = "quantized linear weight requires a valid format and input width divisible by 32"
+    for shape, fmt in (((2, 33), 1), ((2, 64), 3), ((2, 16), 2)):
+        w = np.zeros(shape, np.float16)
+        rok, _, rmsg = ref.quantize(w, fmt)
+        ok, packed, msg = sdk.quantize(w, fmt)
+        assert not rok and not ok and packed is None and msg == rmsg == message
+    result = ctypes.c_void_p(7)
+    err = ctypes.create_string_buffer(256)
+    assert not lib.tensor_quantize_linear_weight_f16(None, 2, 32, 1, ctypes.byref(result), err, 256)
+    assert result.value is None and err.value.decode() == message
 
 
 def test_validation_precedes_device_use(lib):
