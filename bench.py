@@ -295,6 +295,46 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
             lambda s: sdk.call("tensor_embedding_lookup_f16", emb_table, s[0], s[1]),
             2 * tokens * width * 2 + tokens * 4, tokens * width)
     del emb_table
+    # quantized linear (decode GEMV, HBM-bound on the packed weights): a
+    # [28672, 8192] Q8_0 / Q4_0 matrix (a 70B-class MLP up+gate projection)
+    # times 1 or 4 f16 rows; synthetic packed bytes with an f16 scale of 2^-7
+    rng = np.random.default_rng(7)
+    def packed_weights(out, inw, block):
+        raw = rng.integers(0, 256, size=(out, inw // 32, block), dtype=np.uint8)
+        raw[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
+        return raw
+    for fmt, block in (("q8_0", 34), ("q4_0", 18)):
+        out_f, in_f = 28672, 8192
+        host_w = packed_weights(out_f, in_f, block)
+        for rows in ((1, 4) if fmt == "q8_0" else (1,)):
+            def quant_set(rows=rows, host_w=host_w):
+                return (T("u8", host_w.shape).upload(host_w),
+                        filled("f16", (rows, in_f), "normal", 7, 3, 0.0, 1.0),
+                        T("f16", (rows, out_f)))
+            measure(f"linear_{fmt}_f16_{rows}x{in_f}_to_{out_f}", quant_set,
+                    lambda s, fmt=fmt: sdk.call(f"tensor_linear_{fmt}_f16", s[1], s[0], s[2]),
+                    host_w.nbytes + rows * (in_f + out_f) * 2, rows * out_f)
+        del host_w
+    # f16 linear through hipBLASLt: a decode row (HBM-bound GEMV on the
+    # weights) and a 4096-token prefill (MFMA-bound)
+    def linear_set(rows, inw, out_f):
+        return lambda: (filled("f16", (rows, inw), "normal", 8, 0, 0.0, 1.0),
+                        filled("f16", (out_f, inw), "normal", 8, 1, 0.0, 0.02),
+                        filled("f16", (out_f,), "normal", 8, 2, 0.0, 1.0), T("f16", (rows, out_f)))
+    run_linear = lambda s: sdk.call("tensor_linear_f16", s[0], s[1], s[2], s[3])
+    measure("linear_f16_decode_1x8192_to_8192", linear_set(1, 8192, 8192), run_linear,
+            8192 * 8192 * 2 + 2 * 8192 * 2 + 8192 * 2, 8192)
+    rows_p = in_p = out_p = 4096
+    p_flops = 2.0 * rows_p * in_p * out_p
+    p_bytes = (rows_p * in_p + out_p * in_p + rows_p * out_p + out_p) * 2
+    batches, _ = timed(linear_set(rows_p, in_p, out_p), run_linear, p_bytes)
+    best = min(batches)
+    results["linear_f16_prefill_4096x4096_to_4096_bias"] = {
+        "avg_us": round(best * 1e3, 2), "batches_us": [round(t * 1e3, 2) for t in batches],
+        "tflops": round(p_flops / (best * 1e-3) / 1e12, 1),
+        "pct_peak_mfma": round(100 * p_flops / (best * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 1),
+        "peak_tflops": MFMA_PEAK_TFLOPS["f16"], "flops": p_flops, "bytes": p_bytes,
+        "library": "hipBLASLt (bias epilogue)"}
     # attention (MFMA-bound, not HBM): scaled dot-product attention on device
     # buffers; flops = 4 * B * Hq * Lq * Lkv * D (half for causal), against
     # the 2.5 PFLOP/s dense f16 MFMA peak

@@ -7,16 +7,21 @@
 // nibble of byte j, stored as value + 8 (Q4_0, 18 bytes).
 //
 // quant_gemv_kernel: y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
-// A wave owns O output rows; its 64 lanes walk the blocks of those rows
-// (lane l takes blocks l, l+64, ...), so the wave reads each weight row as
-// one contiguous stream. A block starts on a 2-byte boundary: the lane loads
-// the 4-byte words covering it and re-aligns them with v_perm_b32. The int8 /
-// nibble values are turned into exact f16 pairs (0x6400 | byte is 1024 +
-// byte; one packed f16 subtract removes the offset) and multiplied with the
-// x pairs by v_dot2_f32_f16, f32 accumulation. x for the lane's block is
-// loaded once and reused for all O rows. The wave's partial sums are folded
-// with DPP at the end. Bound: HBM bytes of the packed weights (1.0625 or
-// 0.5625 bytes per weight) for small row counts.
+// A wave owns O output rows and walks them in chunks of 64 blocks. Each
+// chunk of each row is a contiguous byte range; the wave reads it with
+// coalesced 16-byte loads (the aligned 16-byte segments covering the range)
+// into its own LDS region, then lane l takes block l of the chunk from LDS:
+// blocks start on 2-byte boundaries, so the lane reads the 4-byte words
+// covering its block and re-aligns them with v_perm_b32. (Loading each
+// lane's block straight from memory -- 34 bytes at a 34-byte lane stride --
+// spreads every load instruction over ~17 cache lines and ran at half the
+// rate.) The int8 / nibble values are turned into exact f16 pairs
+// (0x6400 | byte is 1024 + byte; one packed f16 subtract removes the offset)
+// and multiplied with the x pairs by v_dot2_f32_f16, f32 accumulation; x for
+// the lane's block is loaded once per chunk and reused for all O rows. The
+// wave's partial sums are folded with DPP at the end. Bound: HBM bytes of
+// the packed weights (1.0625 or 0.5625 bytes per weight) at small row
+// counts.
 #include "kern_common.hpp"
 #include "kernels.hpp"
 
@@ -33,28 +38,27 @@ template <bool kQ8> struct Fmt {
 
 __device__ inline half2_t as_half2(uint32_t bits) { return __builtin_bit_cast(half2_t, bits); }
 
-// Loads the block at byte address `addr` (2-byte aligned): its scale and its
-// packed values re-aligned to 4-byte words. Every access stays inside the
-// block or the 2 bytes before it, which share its aligned 4-byte word.
+// Reads the block at byte offset `off` (even) of an LDS chunk: its scale
+// and its packed values re-aligned to 4-byte words. The reads cover the
+// block and at most the 2 bytes before it; both tail reads are
+// unconditional (an aligned block reads its last half-word twice and uses
+// only the low half).
 template <bool kQ8>
-__device__ inline float load_block(const uint8_t *addr, uint32_t (&q)[Fmt<kQ8>::kWords]) {
+__device__ inline float read_block(const uint8_t *chunk, uint32_t off,
+                                   uint32_t (&q)[Fmt<kQ8>::kWords]) {
     constexpr int W = Fmt<kQ8>::kWords;
-    const uintptr_t a = reinterpret_cast<uintptr_t>(addr);
-    const bool shifted = (a & 2) != 0;
-    const uint32_t *words = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    const uint32_t shift = off & 2u;
+    const uint8_t *base = chunk + (off - shift);
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(base);
     uint32_t e[W + 1];
 #pragma unroll
-    for (int i = 0; i < W; ++i) e[i] = __builtin_nontemporal_load(words + i);
-    // word W: its low half is the block's last two bytes when the block is
-    // aligned; a shifted block ends with the whole word
-    const uint16_t *tail = reinterpret_cast<const uint16_t *>(words + W);
-    uint32_t last = tail[0];
-    if (shifted) last |= uint32_t(tail[1]) << 16;
-    e[W] = last;
-    const uint32_t sel = shifted ? 0x07060504u : 0x05040302u;
+    for (int i = 0; i < W; ++i) e[i] = words[i];
+    const uint16_t *tail = reinterpret_cast<const uint16_t *>(base + 4 * W);
+    e[W] = (uint32_t)tail[0] | (uint32_t)tail[shift >> 1] << 16;
+    const uint32_t sel = shift ? 0x07060504u : 0x05040302u;
 #pragma unroll
     for (int i = 0; i < W; ++i) q[i] = __builtin_amdgcn_perm(e[i + 1], e[i], sel);
-    const uint32_t scale_bits = shifted ? (e[0] >> 16) : (e[0] & 0xffffu);
+    const uint32_t scale_bits = shift ? (e[0] >> 16) : (e[0] & 0xffffu);
     return (float)__builtin_bit_cast(_Float16, (uint16_t)scale_bits);
 }
 
@@ -101,20 +105,27 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
                                                             uint16_t *__restrict__ y,
                                                             uint32_t rows, uint32_t in,
                                                             uint32_t out) {
+    constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
+    constexpr uint32_t kChunk = kWave * kBytes;        // bytes of 64 blocks
+    constexpr uint32_t kVecs = kChunk / 16 + 2;        // 16-byte segments covering a chunk
+    constexpr uint32_t kPasses = (kVecs + kWave - 1) / kWave;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kBlock / kWave][O][kVecs * 16];
     const uint32_t lane = threadIdx.x & (kWave - 1);
+    uint8_t (*region)[kVecs * 16] = stage[threadIdx.x / kWave];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(
         (blockIdx.x * kBlock + threadIdx.x) / kWave);
     const uint32_t o0 = wave * O;
     if (o0 >= out) return;
     const uint32_t r0 = blockIdx.y * R;
     const uint32_t blocks = in / 32;
-    const uint64_t row_bytes = (uint64_t)blocks * Fmt<kQ8>::kBytes;
+    const uint64_t row_bytes = (uint64_t)blocks * kBytes;
     // rows past the end are clamped onto the last one (computed, not stored)
-    uint32_t orow[O], xrow[R];
+    const uint8_t *wrow[O];
+    const uint16_t *xrow[R];
 #pragma unroll
-    for (int o = 0; o < O; ++o) orow[o] = min(o0 + o, out - 1);
+    for (int o = 0; o < O; ++o) wrow[o] = w + (uint64_t)min(o0 + o, out - 1) * row_bytes;
 #pragma unroll
-    for (int r = 0; r < R; ++r) xrow[r] = min(r0 + r, rows - 1);
+    for (int r = 0; r < R; ++r) xrow[r] = x + (uint64_t)min(r0 + r, rows - 1) * in;
 
     float acc[O][R];
 #pragma unroll
@@ -122,28 +133,64 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[o][r] = 0.0f;
 
-    for (uint32_t b = lane; b < blocks; b += kWave) {
-        uint32_t q[O][Fmt<kQ8>::kWords];
-        float scale[O];
+    for (uint32_t c0 = 0; c0 < blocks; c0 += kWave) {
+        const uint32_t nb = min((uint32_t)kWave, blocks - c0);
+        // the aligned 16-byte segments holding this chunk of each row; a
+        // segment never crosses a page, so the bytes around the chunk that
+        // share its first and last segment are safe to read
+        uint32_t lead[O];
+        u32x4 seg[O][kPasses];
 #pragma unroll
-        for (int o = 0; o < O; ++o)
-            scale[o] = load_block<kQ8>(w + orow[o] * row_bytes + (uint64_t)b * Fmt<kQ8>::kBytes, q[o]);
+        for (int o = 0; o < O; ++o) {
+            const uint8_t *start = wrow[o] + (uint64_t)c0 * kBytes;
+            lead[o] = (uint32_t)(reinterpret_cast<uintptr_t>(start) & 15u);
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(start - lead[o]);
+            const uint32_t nvec = (lead[o] + nb * kBytes + 15) / 16;
+#pragma unroll
+            for (int i = 0; i < (int)kPasses; ++i) {
+                const uint32_t v = lane + kWave * i;
+                seg[o][i] = v < nvec ? __builtin_nontemporal_load(src + v) : u32x4{0, 0, 0, 0};
+            }
+        }
+        const uint32_t b = c0 + min(lane, nb - 1);
+        uint32_t xv[R][16];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const u32x4 *xp = reinterpret_cast<const u32x4 *>(x + (uint64_t)xrow[r] * in + b * 32);
-            uint32_t xv[16];
+            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow[r] + (uint64_t)b * 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const u32x4 t = xp[v];
-                xv[4 * v] = t.x;
-                xv[4 * v + 1] = t.y;
-                xv[4 * v + 2] = t.z;
-                xv[4 * v + 3] = t.w;
+                xv[r][4 * v] = t.x;
+                xv[r][4 * v + 1] = t.y;
+                xv[r][4 * v + 2] = t.z;
+                xv[r][4 * v + 3] = t.w;
             }
-#pragma unroll
-            for (int o = 0; o < O; ++o)
-                acc[o][r] = __builtin_fmaf(scale[o], block_dot<kQ8>(q[o], xv), acc[o][r]);
         }
+#pragma unroll
+        for (int o = 0; o < O; ++o)
+#pragma unroll
+            for (int i = 0; i < (int)kPasses; ++i) {
+                const uint32_t v = lane + kWave * i;
+                if (v < kVecs) *reinterpret_cast<u32x4 *>(&region[o][v * 16]) = seg[o][i];
+            }
+        // the region is this wave's alone: order its LDS writes before the
+        // reads of other lanes, and the reads before the next chunk's writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const bool live = lane < nb;
+#pragma unroll
+        for (int o = 0; o < O; ++o) {
+            uint32_t q[Fmt<kQ8>::kWords];
+            const float scale = read_block<kQ8>(region[o], lead[o] + (b - c0) * kBytes, q);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float part = scale * block_dot<kQ8>(q, xv[r]);
+                acc[o][r] += live ? part : 0.0f;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
     for (int o = 0; o < O; ++o)
@@ -302,17 +349,17 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
         hipError_t status;
         size_t done;
         if (left <= 1) {
-            status = launch_gemv<kQ8, 1, 2>(xr, w, yr, left, in, out, s);
+            status = launch_gemv<kQ8, 1, kQ8 ? 4 : 2>(xr, w, yr, left, in, out, s);
             done = left;
         } else if (left <= 2) {
-            status = launch_gemv<kQ8, 2, 2>(xr, w, yr, left, in, out, s);
+            status = launch_gemv<kQ8, 2, 4>(xr, w, yr, left, in, out, s);
             done = left;
         } else if (left <= 4) {
-            status = launch_gemv<kQ8, 4, 1>(xr, w, yr, left, in, out, s);
+            status = launch_gemv<kQ8, 4, 4>(xr, w, yr, left, in, out, s);
             done = left;
         } else {
             done = left < kMaxGroups * 8 ? left : kMaxGroups * 8;
-            status = launch_gemv<kQ8, 8, 1>(xr, w, yr, done, in, out, s);
+            status = launch_gemv<kQ8, 8, 2>(xr, w, yr, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;
