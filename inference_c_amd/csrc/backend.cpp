@@ -14,6 +14,7 @@
 // overflow); a failed check returns 0.
 #include "gemm.hpp"
 #include "kernels.hpp"
+#include "pinned.hpp"
 #include "sdk.hpp"
 #include "staging.hpp"
 
@@ -454,6 +455,7 @@ void release_cache(void) {
     scratch_clear();
     weight_cache_clear();
     gemm_release();
+    pinned_release();
 }
 
 // Device-resident slots: raw device addresses, enqueue only.

@@ -6,6 +6,7 @@
 // and kernel is ordered on one non-blocking SDK stream created at first use;
 // uploads and downloads synchronise that stream before returning, D2D copies
 // only enqueue, and tensor_device_synchronize waits for the stream.
+#include "pinned.hpp"
 #include "sdk.hpp"
 
 #include "kernels.hpp"
@@ -153,8 +154,7 @@ void *weight_cache_get(const void *host, size_t bytes) {
     bind_device();
     void *device = nullptr;
     if (hipMalloc(&device, bytes) != hipSuccess) return nullptr;
-    if (hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, state().stream) !=
-        hipSuccess) {
+    if (!pinned_to_device(device, host, bytes, state().stream, nullptr, 0)) {
         (void)hipStreamSynchronize(state().stream);
         (void)hipFree(device);
         return nullptr;
@@ -288,11 +288,10 @@ extern "C" int tensor_device_buffer_upload(TensorDeviceBuffer *destination,
     }
     if (byte_length == 0) return 1;
     if (!sdk_ready(error, error_capacity)) return 0;
-    return hip_ok(hipMemcpyAsync(static_cast<char *>(destination->data) + destination_offset,
-                                 source, byte_length, hipMemcpyHostToDevice, sdk_stream()),
-                  "hipMemcpyAsync host-to-device", error, error_capacity) &&
-           hip_ok(hipStreamSynchronize(sdk_stream()), "hipStreamSynchronize", error,
-                  error_capacity);
+    // the source has been read into pinned chunks when this returns; the
+    // device copy completes in stream order
+    return pinned_to_device(static_cast<char *>(destination->data) + destination_offset, source,
+                            byte_length, sdk_stream(), error, error_capacity);
 }
 
 extern "C" int tensor_device_buffer_download(const TensorDeviceBuffer *source,
@@ -306,12 +305,8 @@ extern "C" int tensor_device_buffer_download(const TensorDeviceBuffer *source,
     }
     if (byte_length == 0) return 1;
     if (!sdk_ready(error, error_capacity)) return 0;
-    return hip_ok(hipMemcpyAsync(destination,
-                                 static_cast<const char *>(source->data) + source_offset,
-                                 byte_length, hipMemcpyDeviceToHost, sdk_stream()),
-                  "hipMemcpyAsync device-to-host", error, error_capacity) &&
-           hip_ok(hipStreamSynchronize(sdk_stream()), "hipStreamSynchronize", error,
-                  error_capacity);
+    return pinned_to_host(destination, static_cast<const char *>(source->data) + source_offset,
+                          byte_length, sdk_stream(), error, error_capacity);
 }
 
 extern "C" int tensor_device_buffer_copy(TensorDeviceBuffer *destination,

@@ -1,12 +1,14 @@
 // Operand binding for one library call.
 //
 // Device operands are used in place. Host operands are staged through the
-// device pool: inputs are copied in on the SDK stream before the kernel,
-// outputs copied back after it, and finish() waits for the stream so the
-// host memory is written when the call returns. Any HIP failure is recorded
-// once and reported by finish().
+// device pool: inputs are copied in on the SDK stream before the kernel
+// (through pinned chunks, so the caller's memory has been read when bind
+// returns), outputs are copied back after it, and finish() returns once the
+// host memory is written. Any HIP failure is recorded once and reported by
+// finish().
 #pragma once
 
+#include "pinned.hpp"
 #include "sdk.hpp"
 
 #include <stddef.h>
@@ -20,8 +22,9 @@ public:
     Staging(const Staging &) = delete;
     Staging &operator=(const Staging &) = delete;
     ~Staging() {
-        // an abandoned host call may still have copies in flight from or to
-        // caller memory: drain them before the staging blocks are reused
+        // an abandoned host call may still have kernels in flight on its
+        // staging blocks; later users of the blocks enqueue after them on the
+        // same stream, but drain anyway so a failed call leaves nothing behind
         if (host_ && count_ > 0 && !synced_) (void)hipStreamSynchronize(stream_);
         for (int i = 0; i < count_; ++i) scratch_release(slots_[i].device, slots_[i].pooled);
     }
@@ -49,14 +52,18 @@ public:
             return false;
         }
         if (host_) {
+            bool copied = false;
             for (int i = 0; i < count_; ++i) {
                 if (!slots_[i].copy_out || slots_[i].bytes == 0) continue;
-                if (!check(hipMemcpyAsync(slots_[i].host, slots_[i].device, slots_[i].bytes,
-                                          hipMemcpyDeviceToHost, stream_),
-                           "device-to-host copy"))
+                if (!pinned_to_host(slots_[i].host, slots_[i].device, slots_[i].bytes, stream_,
+                                    error_, capacity_)) {
+                    failed_ = true;
                     return false;
+                }
+                copied = true;
             }
-            synced_ = check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+            // each output copy waited for the work before it; with none, wait here
+            synced_ = copied || check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
             return synced_;
         }
         return true;
@@ -89,9 +96,10 @@ private:
         }
         slots_[count_++] = Slot{data, device, bytes, size, copy_out};
         if (copy_in && bytes > 0 &&
-            !check(hipMemcpyAsync(device, data, bytes, hipMemcpyHostToDevice, stream_),
-                   "host-to-device copy"))
+            !pinned_to_device(device, data, bytes, stream_, error_, capacity_)) {
+            failed_ = true;
             return nullptr;
+        }
         return device;
     }
 

@@ -88,3 +88,76 @@ def test_backend_selection(sdk, monkeypatch):
 
 def test_stream_is_exposed(sdk):
     assert sdk.stream() != 0
+
+
+# ---- pinned staging ----------------------------------------------------------
+# Host memory crosses PCIe through 4 MiB page-locked chunks (at most three per
+# transfer, reused in rotation). Sizes below straddle every chunk boundary
+# case: sub-chunk, exactly one chunk, one chunk plus a tail, several chunks
+# reusing the same three.
+
+STAGING_SIZES = [1, 4095, (1 << 20) + 1, 4 << 20, (4 << 20) + 3, (13 << 20) + 7, (9 << 20) + 1, 40 << 20]
+
+
+@pytest.mark.parametrize("nbytes", STAGING_SIZES)
+def test_pinned_round_trip(sdk, nbytes):
+    rng = np.random.default_rng(nbytes)
+    data = rng.integers(0, 256, nbytes, dtype=np.uint8)
+    t = sdk.tensor("u8", (nbytes,)).upload(data)
+    data_copy = data.copy()
+    data[:] = 0  # the upload has consumed the source when it returns
+    assert np.array_equal(t.download(), data_copy)
+
+
+def test_pinned_upload_at_offsets(sdk):
+    """Uploads and downloads of sub-ranges at odd offsets."""
+    rng = np.random.default_rng(7)
+    total = (9 << 20) + 5
+    t = sdk.tensor("u8", (total,))
+    want = np.zeros(total, np.uint8)
+    t.upload(want)
+    err = ctypes.create_string_buffer(256)
+    for offset, length in ((3, 17), (1 << 20, (5 << 20) + 1), (total - 9, 9), (0, total)):
+        part = rng.integers(0, 256, length, dtype=np.uint8)
+        assert sdk.lib.tensor_buffer_upload(t.handle, offset, part.ctypes.data, length, err, 256)
+        want[offset:offset + length] = part
+        got = np.empty(length, np.uint8)
+        assert sdk.lib.tensor_buffer_download(t.handle, offset, got.ctypes.data, length, err, 256)
+        assert np.array_equal(got, part)
+    assert np.array_equal(t.download(), want)
+
+
+def test_host_slots_from_several_threads(sdk, orc):
+    """Host-pointer slots called concurrently from 4 threads, each moving
+    several chunks per call: every result matches the oracle bit for bit."""
+    import threading
+    from tests.test_gpu_vtable import Table
+    table = ctypes.cast(sdk.lib.tensor_compute_hip_backend(), ctypes.POINTER(Table)).contents
+    fn = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                          ctypes.c_size_t)(table.residual_add_f16)
+    sizes = [(3 << 20) + 1, (6 << 20) + 11, 777, (9 << 20) + 3]
+    inputs = [(orc.normal((n,), 80 + i, 0, 0.0, 1.0, "f16"), orc.normal((n,), 80 + i, 1, 0.0, 1.0, "f16"))
+              for i, n in enumerate(sizes)]
+    wants = [orc.add(a, b) for a, b in inputs]
+    failures = []
+
+    def work(i):
+        a, b = inputs[i]
+        for _ in range(3):
+            y = np.empty_like(a)
+            if not fn(a.ctypes.data, b.ctypes.data, y.ctypes.data, a.size):
+                failures.append((i, "call failed"))
+            elif not np.array_equal(y.view(np.uint16), wants[i].view(np.uint16)):
+                failures.append((i, "wrong result"))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(sizes))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not failures, failures
+    ctypes.CFUNCTYPE(None)(table.release_cache)()
+    # the pool is rebuilt on the next call
+    y = np.empty_like(inputs[0][0])
+    assert fn(inputs[0][0].ctypes.data, inputs[0][1].ctypes.data, y.ctypes.data, sizes[0])
+    assert np.array_equal(y.view(np.uint16), wants[0].view(np.uint16))
