@@ -335,6 +335,29 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
         "pct_peak_mfma": round(100 * p_flops / (best * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 1),
         "peak_tflops": MFMA_PEAK_TFLOPS["f16"], "flops": p_flops, "bytes": p_bytes,
         "library": "hipBLASLt (bias epilogue)"}
+    # host-pointer compute-table slot (PCIe included, never `value`): SwiGLU
+    # on cfg2's [4096, 16384] f16 operands in pageable host memory, staged
+    # through the pinned chunk pool; wall clock of the synchronous call
+    import ctypes as _ct
+    table = sdk.compute_table()
+    slot = _ct.CFUNCTYPE(_ct.c_int, _ct.c_void_p, _ct.c_void_p, _ct.c_void_p,
+                         _ct.c_size_t)(table.silu_multiply_f16)
+    n_host = 4096 * 16384
+    ha = np.random.default_rng(1).standard_normal(n_host).astype(np.float16)
+    hb = np.random.default_rng(2).standard_normal(n_host).astype(np.float16)
+    hy = np.empty_like(ha)
+    assert slot(ha.ctypes.data, hb.ctypes.data, hy.ctypes.data, n_host)
+    walls = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        assert slot(ha.ctypes.data, hb.ctypes.data, hy.ctypes.data, n_host)
+        walls.append(time.perf_counter() - t0)
+    wall = statistics.median(walls)
+    results["host_slot_swiglu_f16_pcie"] = {
+        "wall_us": round(wall * 1e6, 1), "bytes": 3 * 2 * n_host,
+        "gbps_pcie_inclusive": round(3 * 2 * n_host / wall / 1e9, 2),
+        "note": "inputs and output in pageable host memory; median of 5 synchronous calls"}
+    del ha, hb, hy
     # attention (MFMA-bound, not HBM): scaled dot-product attention on device
     # buffers; flops = 4 * B * Hq * Lq * Lkv * D (half for causal), against
     # the 2.5 PFLOP/s dense f16 MFMA peak

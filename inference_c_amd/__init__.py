@@ -4,5 +4,5 @@ The product is the C-ABI library libinference_sdk_hip.so built from csrc/
 (declarations in include/*.h at the repository root). This package only
 locates and binds it: see sdk.py.
 """
-from .sdk import (DEVICE, HOST, LIB_PATH, Sdk, SdkError, Tensor, TensorView,  # noqa: F401
+from .sdk import (COMPUTE_SLOTS, DEVICE, HOST, LIB_PATH, ComputeBackend, Sdk, SdkError, Tensor, TensorView,  # noqa: F401
                   declared_functions, load_library)

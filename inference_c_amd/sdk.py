@@ -63,6 +63,29 @@ OP_ARGTYPES = {
 }
 
 
+# TensorComputeBackend (include/tensor_compute_backend.h) field order: the
+# name, then one function pointer per slot.
+COMPUTE_SLOTS = [
+    "name", "is_available", "linear_f32", "linear_f16", "embedding_f16", "rms_norm_f16",
+    "layer_norm_f16", "bias_add_f16", "gelu_f16", "gelu_multiply_f16", "relu_f16",
+    "rope_f16", "silu_multiply_f16", "residual_add_f16", "argmax_f16", "embedding_f32",
+    "rms_norm_f32", "rms_norm_linear_f32", "layer_norm_f32", "bias_add_f32", "gelu_f32",
+    "rope_f32", "silu_multiply_f32", "residual_add_f32", "argmax_f32", "release_cache",
+    "mlp_f32", "mlp_f16", "qkv_f16", "vision_layer_f16", "vision_layer_f32",
+    "vision_sequence_begin_f16", "vision_sequence_layer_f16", "vision_sequence_finish_f16",
+    "vision_sequence_release_f16", "vision_sequence_layer_quant_f16",
+    "vision_sequence_begin_f32", "vision_sequence_layer_f32", "vision_sequence_finish_f32",
+    "vision_sequence_release_f32", "linear_f32_device", "linear_f16_device",
+    "linear_q8_0_f16_device", "linear_q4_0_f16_device", "linear_q8_0_f16",
+    "linear_q4_0_f16", "bias_add_f32_device", "bias_add_f16_device",
+    "residual_add_f16_device"]
+
+
+class ComputeBackend(ctypes.Structure):
+    """TensorComputeBackend as raw addresses (NULL slots read as None)."""
+    _fields_ = [(s, ctypes.c_void_p) for s in COMPUTE_SLOTS]
+
+
 class SdkError(RuntimeError):
     """A library call returned 0; the message is the library's error text."""
 
@@ -258,6 +281,11 @@ class Sdk:
             return 1, packed, ""
         finally:
             self.lib.tensor_buffer_free(result)
+
+    def compute_table(self) -> ComputeBackend:
+        """The library's "hip" TensorComputeBackend."""
+        return ctypes.cast(self.lib.tensor_compute_hip_backend(),
+                           ctypes.POINTER(ComputeBackend)).contents
 
     def synchronize(self) -> None:
         self.call("tensor_device_synchronize")

@@ -13,19 +13,8 @@ from tests.helpers import arbitrated, assert_bits_equal, assert_f16_ulps, f16_ul
 
 pytestmark = pytest.mark.gpu
 
-SLOTS = ["name", "is_available", "linear_f32", "linear_f16", "embedding_f16", "rms_norm_f16",
-         "layer_norm_f16", "bias_add_f16", "gelu_f16", "gelu_multiply_f16", "relu_f16",
-         "rope_f16", "silu_multiply_f16", "residual_add_f16", "argmax_f16", "embedding_f32",
-         "rms_norm_f32", "rms_norm_linear_f32", "layer_norm_f32", "bias_add_f32", "gelu_f32",
-         "rope_f32", "silu_multiply_f32", "residual_add_f32", "argmax_f32", "release_cache",
-         "mlp_f32", "mlp_f16", "qkv_f16", "vision_layer_f16", "vision_layer_f32",
-         "vision_sequence_begin_f16", "vision_sequence_layer_f16", "vision_sequence_finish_f16",
-         "vision_sequence_release_f16", "vision_sequence_layer_quant_f16",
-         "vision_sequence_begin_f32", "vision_sequence_layer_f32", "vision_sequence_finish_f32",
-         "vision_sequence_release_f32", "linear_f32_device", "linear_f16_device",
-         "linear_q8_0_f16_device", "linear_q4_0_f16_device", "linear_q8_0_f16",
-         "linear_q4_0_f16", "bias_add_f32_device", "bias_add_f16_device",
-         "residual_add_f16_device"]
+from inference_c_amd import COMPUTE_SLOTS as SLOTS  # noqa: E402
+
 
 P, Z, F, D, I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float, ctypes.c_double, ctypes.c_int
 SIGS = {
@@ -42,8 +31,7 @@ SIGS = {
 }
 
 
-class Table(ctypes.Structure):
-    _fields_ = [(s, ctypes.c_void_p) for s in SLOTS]
+from inference_c_amd import ComputeBackend as Table  # noqa: E402,F401
 
 
 @pytest.fixture(scope="module")
