@@ -75,7 +75,7 @@ class Hip:
         assert self.lib.hipMemsetAsync(ptr, 0, nbytes, stream) == 0
 
 
-TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "cfg2_hbm_traffic.md")
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "cfg2_and_q8_gemv_hbm_traffic.md")
 
 
 def measured_traffic(kernel):
@@ -417,6 +417,16 @@ def pmc_probe(sdk, reps=3):
            ("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x"], t["y"])),
            ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x"], t["y"])),
            ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
+    # the Q8_0 decode GEMV of the suite: [28672, 8192] packed weights, one row
+    import numpy as np
+    packed = np.random.default_rng(7).integers(0, 256, size=(28672, 256, 34), dtype=np.uint8)
+    packed[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
+    t["w8"] = sdk.tensor("u8", packed.shape).upload(packed)
+    t["x8"], t["y8"] = sdk.tensor("f16", (1, 8192)), sdk.tensor("f16", (1, 28672))
+    sdk.call("tensor_fill_normal", t["x8"], 7, 3, 0.0, 1.0)
+    del packed
+    ops.append(("linear_q8_0_f16_1x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
     for name, fn in ops:
         for _ in range(reps):
             sdk.call("tensor_fill_uniform", flush, 7, 0, -1.0, 1.0)
@@ -433,7 +443,8 @@ def main():
     ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only run the counter-collection workload (copy + cfg2 kernels)")
+                    help="only run the counter-collection workload (copy, cfg2 kernels and "
+                         "the Q8_0 decode GEMV)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one "

@@ -387,6 +387,199 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
         }
 }
 
+// f32 flash kernel (D = Dv in {64, 128}): v_mfma_f32_32x32x2_f32, one wave
+// per 32 queries, BM queries per block, 32-key K and V tiles in LDS
+// (row-major, row pitch D + 4 floats: conflict-free 16-byte reads),
+// double-buffered.
+//   S^T = K Q^T: MFMA c contracts the d pair {c, D/2 + c}: lane half h holds
+//   d in [h D/2, (h + 1) D/2), so each lane's K and Q operands are runs of
+//   consecutive floats (Q stays in registers for the whole kernel).
+//   out^T += V^T P^T: MFMA j contracts the key pair {8(j/4) + j%4, that + 4},
+//   exactly the keys that accumulator register j of S^T holds in the two lane
+//   halves, so P is the B operand as it stands and V needs no transpose.
+// Scores are s * scale (+ mask), causal keys -inf; the online softmax uses
+// expf (libm accuracy) and normalises once at the end by the reciprocal of
+// the sum, with the special-row rules of the f16 kernel.
+constexpr int kFlashN32 = 32;   // keys per f32 tile
+
+template <int D, int BM, bool kMask>
+__global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__restrict__ q,
+                                                                const float *__restrict__ k,
+                                                                const float *__restrict__ v,
+                                                                const float *__restrict__ mask,
+                                                                float *__restrict__ out,
+                                                                SdpaArgs a) {
+    constexpr int THREADS = BM * 2;
+    constexpr int KN = kFlashN32;
+    constexpr int ROW = D + 4;               // LDS row (floats)
+    constexpr int VT = D / 32;               // 32-row tiles of out^T
+    constexpr int QC = D / 2;                // MFMAs of S^T per tile
+    constexpr int VECS = KN * D / 4;         // float4 vectors per K or V tile
+    constexpr int PER = VECS / THREADS;
+    static_assert(VECS % THREADS == 0, "tile load split");
+    __shared__ __attribute__((aligned(16))) float ks[2][KN * ROW];
+    __shared__ __attribute__((aligned(16))) float vs[2][KN * ROW];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint32_t col = lane & 31, half = lane >> 5;
+    const uint32_t qblocks = (a.ql + BM - 1) / BM;
+    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
+    const uint32_t qblock = logical % qblocks;
+    const uint32_t bh = logical / qblocks;
+    const uint32_t head = bh % a.qh, b = bh / a.qh;
+    const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
+    const uint32_t qw = qblock * BM + wave * 32;
+    const uint32_t qi = qw + col;
+    const bool q_live = qi < a.ql;
+    const float neg_inf = -__builtin_inff();
+
+    float qf[QC];
+    {
+        const f32x4 *qrow = reinterpret_cast<const f32x4 *>(
+            q + ((size_t)bh * a.ql + (q_live ? qi : 0)) * D + half * QC);
+#pragma unroll
+        for (int c = 0; c < QC / 4; ++c) {
+            const f32x4 t = qrow[c];
+            qf[4 * c] = t.x;
+            qf[4 * c + 1] = t.y;
+            qf[4 * c + 2] = t.z;
+            qf[4 * c + 3] = t.w;
+        }
+    }
+    float16v o[VT];
+#pragma unroll
+    for (int t = 0; t < VT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+    float m = neg_inf, l = 0.0f;
+    bool nan_seen = false;
+
+    const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
+    const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
+                                      : (uint64_t)a.kl;
+    const uint32_t tiles = (uint32_t)((key_end + KN - 1) / KN);
+    const bool wave_live = qw < a.ql;
+    const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
+    const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
+
+    // tile loads: vector e of a tile is key e / (D/4), floats 4 (e % (D/4)) ...
+    f32x4 kreg[PER], vreg[PER];
+    auto fetch = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t e = tid + u * THREADS;
+            const uint32_t kk = k0 + e / (D / 4), part = e % (D / 4);
+            const size_t at = (kv_base + kk) * D + part * 4;
+            kreg[u] = kk < a.kl ? *reinterpret_cast<const f32x4 *>(k + at) : f32x4{0, 0, 0, 0};
+            vreg[u] = kk < a.kl ? *reinterpret_cast<const f32x4 *>(v + at) : f32x4{0, 0, 0, 0};
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const uint32_t e = tid + u * THREADS;
+            const uint32_t at = (e / (D / 4)) * ROW + (e % (D / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(&ks[buf][at]) = kreg[u];
+            *reinterpret_cast<f32x4 *>(&vs[buf][at]) = vreg[u];
+        }
+    };
+
+    if (tiles > 0) {
+        fetch(0);
+        stash(0);
+    }
+    __syncthreads();
+    for (uint32_t t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        const uint32_t k0 = t * KN;
+        const bool more = t + 1 < tiles;
+        if (more) fetch(k0 + KN);
+        if (wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
+            const bool interior = k0 + KN <= a.kl &&
+                                  (!a.causal || (uint64_t)k0 + KN - 1 <= (uint64_t)qw + a.causal_offset);
+            // two accumulators (even and odd d pairs) keep two MFMA chains in flight
+            float16v acc[2];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[h2][r] = 0.0f;
+            const float *krow = &ks[buf][col * ROW + half * QC];
+#pragma unroll
+            for (int c4 = 0; c4 < QC / 4; ++c4) {
+                const f32x4 kf = *reinterpret_cast<const f32x4 *>(krow + 4 * c4);
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[4 * c4], acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[4 * c4 + 1], acc[1], 0, 0, 0);
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[4 * c4 + 2], acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[4 * c4 + 3], acc[1], 0, 0, 0);
+            }
+            float st[16];
+            float local_max = neg_inf;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t kk = k0 + 8 * (r / 4) + 4 * half + r % 4;
+                float s = (acc[0][r] + acc[1][r]) * a.scale;
+                if constexpr (kMask) {
+                    if (kk < a.kl && q_live) s = s + mask[(size_t)qi * a.kl + kk];
+                }
+                if (!interior && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
+                    s = neg_inf;
+                st[r] = s;
+                local_max = fmaxf(local_max, s);
+            }
+            const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
+            const bool none = m_new == neg_inf;
+            if (wave_any(none)) {
+                bool local_nan = false;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) local_nan = local_nan || st[r] != st[r];
+                nan_seen = nan_seen || (none && local_nan);
+            }
+            const float alpha = none ? 1.0f : expf(m - m_new);
+            float local_sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                st[r] = none ? 0.0f : expf(st[r] - m_new);
+                local_sum += st[r];
+            }
+            l = l * alpha + (local_sum + __shfl_xor(local_sum, 32, kWave));
+            m = m_new;
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+                for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
+            }
+            // the VT output tiles are independent chains: issue them side by side
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float *vrow = &vs[buf][(8 * (j / 4) + 4 * half + j % 4) * ROW + col];
+#pragma unroll
+                for (int tt = 0; tt < VT; ++tt)
+                    o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * tt], st[j], o[tt], 0, 0, 0);
+            }
+        }
+        if (more) stash(buf ^ 1);
+        __syncthreads();
+    }
+    nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
+    if (!q_live) return;
+    const bool zero = !__builtin_isfinite(m);
+    const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
+    const float nan = __builtin_nanf("");
+    float *orow = out + ((size_t)bh * a.ql + qi) * D;
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 quad;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                quad[j] = zero ? 0.0f : nan_seen ? nan : o[tt][4 * g + j] * inverse;
+            *reinterpret_cast<f32x4 *>(orow + 32 * tt + 8 * g + 4 * half) = quad;
+        }
+}
+
 template <typename S>
 hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out,
                        const k::SdpaShape &sh, float scale, bool causal, hipStream_t s) {
@@ -433,6 +626,47 @@ namespace k {
 hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
                     float *out, const SdpaShape &shape, float scale, bool causal,
                     hipStream_t s) {
+    const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
+    const uint64_t lim = 0x7fffffffull;
+    if (aligned && shape.head_dim == shape.value_dim &&
+        (shape.head_dim == 64 || shape.head_dim == 128) && shape.batch && shape.q_heads &&
+        shape.kv_heads && shape.q_heads % shape.kv_heads == 0 && shape.q_len &&
+        shape.q_len <= lim && shape.kv_len && shape.kv_len <= lim &&
+        shape.batch * shape.q_heads * ((shape.q_len + 63) / 64) <= 0x7fffffffull) {
+        SdpaArgs a{};
+        a.batch = (uint32_t)shape.batch;
+        a.qh = (uint32_t)shape.q_heads;
+        a.kvh = (uint32_t)shape.kv_heads;
+        a.group = (uint32_t)(shape.q_heads / shape.kv_heads);
+        a.ql = (uint32_t)shape.q_len;
+        a.kl = (uint32_t)shape.kv_len;
+        a.dim = a.vdim = (uint32_t)shape.head_dim;
+        a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
+        a.scale = scale;
+        a.causal = causal ? 1 : 0;
+        const size_t bhs = shape.batch * shape.q_heads;
+        const bool wide = ((shape.q_len + 127) / 128) * bhs >= 512;
+        const size_t gx = (shape.q_len + (wide ? 127 : 63)) / (wide ? 128 : 64);
+        const dim3 grid((unsigned)(gx * bhs)), block(wide ? 256 : 128);
+#define ICSDK_FLASH32(D, BM)                                                                      \
+    do {                                                                                          \
+        if (mask)                                                                                 \
+            hipLaunchKernelGGL((sdpa_flash_f32_kernel<D, BM, true>), grid, block, 0, s, q, k, v,    \
+                               mask, out, a);                                                     \
+        else                                                                                      \
+            hipLaunchKernelGGL((sdpa_flash_f32_kernel<D, BM, false>), grid, block, 0, s, q, k, v,   \
+                               mask, out, a);                                                     \
+    } while (0)
+        if (shape.head_dim == 64) {
+            if (wide) ICSDK_FLASH32(64, 128);
+            else ICSDK_FLASH32(64, 64);
+        } else {
+            if (wide) ICSDK_FLASH32(128, 128);
+            else ICSDK_FLASH32(128, 64);
+        }
+#undef ICSDK_FLASH32
+        return hipGetLastError();
+    }
     return launch_sdpa<float>(q, k, v, mask, out, shape, scale, causal, s);
 }
 
