@@ -73,17 +73,20 @@ int host_run(const T *q, const T *k, const T *v, const T *mask, T *out, size_t b
     const void *pm = mask ? st.in(mask, c.mask * sizeof(T)) : nullptr;
     void *po = st.out(out, c.out * sizeof(T));
     if (st.failed()) return 0;
+    ScratchBlock workspace(k::sdpa_workspace_bytes(shape));
+    const size_t ws_bytes = workspace.get() ? k::sdpa_workspace_bytes(shape) : 0;
     hipError_t status;
     if constexpr (sizeof(T) == 4)
         status = k::sdpa_f32(static_cast<const float *>(pq), static_cast<const float *>(pk),
                              static_cast<const float *>(pv), static_cast<const float *>(pm),
-                             static_cast<float *>(po), shape, scale, causal != 0, st.stream());
+                             static_cast<float *>(po), shape, scale, causal != 0,
+                             workspace.get(), ws_bytes, st.stream());
     else
         status = k::sdpa_f16(static_cast<const uint16_t *>(pq),
                              static_cast<const uint16_t *>(pk),
                              static_cast<const uint16_t *>(pv),
                              static_cast<const uint16_t *>(pm), static_cast<uint16_t *>(po),
-                             shape, scale, causal != 0, st.stream());
+                             shape, scale, causal != 0, workspace.get(), ws_bytes, st.stream());
     return st.finish(status) ? 1 : 0;
 }
 
@@ -163,18 +166,22 @@ int sdpa_device(TensorDType dtype, const TensorBuffer *q, const TensorBuffer *k,
     auto dev = [](const TensorBuffer *t) -> void * {
         return t ? tensor_buffer_device_handle_internal(t) : nullptr;
     };
+    // split-key partials live in a pool block, returned right after the
+    // launches (later users of the block enqueue behind them on the stream)
+    ScratchBlock workspace(k::sdpa_workspace_bytes(shape));
+    const size_t ws_bytes = workspace.get() ? k::sdpa_workspace_bytes(shape) : 0;
     const hipError_t status =
         dtype == TENSOR_DTYPE_F32
             ? k::sdpa_f32(static_cast<const float *>(dev(q)), static_cast<const float *>(dev(k)),
                           static_cast<const float *>(dev(v)),
                           static_cast<const float *>(dev(mask)), static_cast<float *>(dev(out)),
-                          shape, scale, causal != 0, sdk_stream())
+                          shape, scale, causal != 0, workspace.get(), ws_bytes, sdk_stream())
             : k::sdpa_f16(static_cast<const uint16_t *>(dev(q)),
                           static_cast<const uint16_t *>(dev(k)),
                           static_cast<const uint16_t *>(dev(v)),
                           static_cast<const uint16_t *>(dev(mask)),
                           static_cast<uint16_t *>(dev(out)), shape, scale, causal != 0,
-                          sdk_stream());
+                          workspace.get(), ws_bytes, sdk_stream());
     return hip_ok(status, "device SDPA: kernel launch", error, capacity) ? 1 : 0;
 }
 

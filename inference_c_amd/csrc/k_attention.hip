@@ -34,6 +34,12 @@ struct SdpaArgs {
     uint32_t causal_offset;           // kl > ql ? kl - ql : 0
     float scale;
     int causal;
+    // split key range (flash kernels): `splits` blocks share one query block,
+    // each writes its unnormalised output rows to part_o[split][row][D] and
+    // {running max, sum, NaN flag, 0} to part_ml[split][row]
+    uint32_t splits;
+    float *part_o;
+    f32x4 *part_ml;
 };
 
 __device__ inline float broadcast_lane(float v, int lane) {
@@ -196,7 +202,69 @@ __device__ inline uint32_t vt_slot(uint32_t key) {
     return (key / 16) * 16 + 8 * ((within / 4) % 2) + (within / 8) * 4 + within % 4;
 }
 
-template <int D, int BM, bool kMask>
+// A split block's result for one query: its lane pair holds the query's
+// unnormalised output rows (out^T accumulator layout), the running max and
+// sum, and the NaN flag.
+template <int D, int VT>
+__device__ inline void write_partial(const SdpaArgs &a, uint32_t split, size_t row, uint32_t half,
+                                     const float16v (&o)[VT], float m, float l, bool nan_seen) {
+    const size_t rows = (size_t)a.batch * a.qh * a.ql;
+    float *prow = a.part_o + ((size_t)split * rows + row) * D;
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 quad = {o[tt][4 * g], o[tt][4 * g + 1], o[tt][4 * g + 2], o[tt][4 * g + 3]};
+            *reinterpret_cast<f32x4 *>(prow + 32 * tt + 8 * g + 4 * half) = quad;
+        }
+    if (half == 0) a.part_ml[(size_t)split * rows + row] = f32x4{m, l, nan_seen ? 1.0f : 0.0f, 0.0f};
+}
+
+// Merges the splits of each query row: M = max of the splits' maxima; a row
+// whose M is not finite is zero; a NaN flag with a finite M makes the row
+// NaN; otherwise out = (sum_s w_s o_s) * (1 / sum_s w_s l_s) with
+// w_s = exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per
+// 4 output elements.
+template <typename S, bool kLog2>
+__global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__restrict__ out) {
+    const size_t rows = (size_t)a.batch * a.qh * a.ql;
+    const uint32_t groups = a.dim / 4;
+    const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= rows * groups) return;
+    const size_t row = i / groups;
+    const uint32_t g = (uint32_t)(i % groups);
+    float big = -__builtin_inff();
+    bool nan_flag = false;
+    for (uint32_t s = 0; s < a.splits; ++s) {
+        const f32x4 ml = a.part_ml[(size_t)s * rows + row];
+        big = fmaxf(big, ml.x);
+        nan_flag = nan_flag || ml.z != 0.0f;
+    }
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float total = 0.0f;
+    if (__builtin_isfinite(big)) {
+        for (uint32_t s = 0; s < a.splits; ++s) {
+            const f32x4 ml = a.part_ml[(size_t)s * rows + row];
+            // a split that saw no visible key has sum 0 and output 0; every
+            // other split is added even at weight 0, so a NaN it holds stays
+            const float w = ml.x == -__builtin_inff() ? 0.0f
+                            : kLog2 ? __builtin_amdgcn_exp2f(ml.x - big) : expf(ml.x - big);
+            const f32x4 po = *reinterpret_cast<const f32x4 *>(
+                a.part_o + ((size_t)s * rows + row) * a.dim + 4 * g);
+            total += w * ml.y;
+            acc += w * po;
+        }
+    }
+    const bool zero = !__builtin_isfinite(big);
+    const float inverse = total == 0.0f ? 0.0f : 1.0f / total;
+    const float nan = __builtin_nanf("");
+    S *orow = out + row * a.dim + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        orow[j] = (S)(zero ? 0.0f : nan_flag ? nan : acc[j] * inverse);
+}
+
+template <int D, int BM, bool kMask, bool kSplit>
 __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__restrict__ q,
                                                             const _Float16 *__restrict__ k,
                                                             const _Float16 *__restrict__ v,
@@ -204,6 +272,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                                                             _Float16 *__restrict__ out,
                                                             SdpaArgs a) {
     constexpr int THREADS = BM * 2;          // one wave per 32 queries
+    constexpr uint32_t kTileKeys = kFlashN;
     constexpr int KC = D / 16;               // 16-dim chunks of Q K^T
     constexpr int VT = D / 32;               // 32-row tiles of out^T
     constexpr int KROW = D + 8;              // LDS row of K (halves)
@@ -219,8 +288,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     const uint32_t col = lane & 31, half = lane >> 5;
     const uint32_t qblocks = (a.ql + BM - 1) / BM;
     const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-    const uint32_t qblock = logical % qblocks;
-    const uint32_t bh = logical / qblocks;
+    const uint32_t split = kSplit ? logical % a.splits : 0;
+    const uint32_t pair = kSplit ? logical / a.splits : logical;
+    const uint32_t qblock = pair % qblocks;
+    const uint32_t bh = pair / qblocks;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
     const uint32_t qw = qblock * BM + wave * 32;        // the wave's first query
@@ -248,7 +319,11 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
     const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
                                       : (uint64_t)a.kl;
-    const uint32_t tiles = (uint32_t)((key_end + kFlashN - 1) / kFlashN);
+    const uint32_t all_tiles = (uint32_t)((key_end + kFlashN - 1) / kFlashN);
+    // this block's share of the key tiles (all of them unless split)
+    const uint32_t share = kSplit ? (all_tiles + a.splits - 1) / a.splits : all_tiles;
+    const uint32_t t_begin = min(split * share, all_tiles);
+    const uint32_t tiles = min(t_begin + share, all_tiles);
     const bool wave_live = qw < a.ql;
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
     const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
@@ -279,12 +354,12 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
         }
     };
 
-    if (tiles > 0) {
-        fetch(0);
-        stash(0);
+    if (t_begin < tiles) {
+        fetch(t_begin * kTileKeys);
+        stash(t_begin & 1);
     }
     __syncthreads();
-    for (uint32_t t = 0; t < tiles; ++t) {
+    for (uint32_t t = t_begin; t < tiles; ++t) {
         const int buf = t & 1;
         const uint32_t k0 = t * kFlashN;
         const bool more = t + 1 < tiles;
@@ -370,6 +445,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     }
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
     if (!q_live) return;
+    if constexpr (kSplit) {
+        write_partial<D, VT>(a, split, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
+        return;
+    }
     const bool zero = !__builtin_isfinite(m);
     const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
     const float nan = __builtin_nanf("");
@@ -402,7 +481,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
 // the sum, with the special-row rules of the f16 kernel.
 constexpr int kFlashN32 = 32;   // keys per f32 tile
 
-template <int D, int BM, bool kMask>
+template <int D, int BM, bool kMask, bool kSplit>
 __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__restrict__ q,
                                                                 const float *__restrict__ k,
                                                                 const float *__restrict__ v,
@@ -411,6 +490,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
                                                                 SdpaArgs a) {
     constexpr int THREADS = BM * 2;
     constexpr int KN = kFlashN32;
+    constexpr uint32_t kTileKeys = KN;
     constexpr int ROW = D + 4;               // LDS row (floats)
     constexpr int VT = D / 32;               // 32-row tiles of out^T
     constexpr int QC = D / 2;                // MFMAs of S^T per tile
@@ -425,8 +505,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     const uint32_t col = lane & 31, half = lane >> 5;
     const uint32_t qblocks = (a.ql + BM - 1) / BM;
     const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-    const uint32_t qblock = logical % qblocks;
-    const uint32_t bh = logical / qblocks;
+    const uint32_t split = kSplit ? logical % a.splits : 0;
+    const uint32_t pair = kSplit ? logical / a.splits : logical;
+    const uint32_t qblock = pair % qblocks;
+    const uint32_t bh = pair / qblocks;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
     const uint32_t qw = qblock * BM + wave * 32;
@@ -458,7 +540,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
     const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
                                       : (uint64_t)a.kl;
-    const uint32_t tiles = (uint32_t)((key_end + KN - 1) / KN);
+    const uint32_t all_tiles = (uint32_t)((key_end + KN - 1) / KN);
+    const uint32_t share = kSplit ? (all_tiles + a.splits - 1) / a.splits : all_tiles;
+    const uint32_t t_begin = min(split * share, all_tiles);
+    const uint32_t tiles = min(t_begin + share, all_tiles);
     const bool wave_live = qw < a.ql;
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
     const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
@@ -485,12 +570,12 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
         }
     };
 
-    if (tiles > 0) {
-        fetch(0);
-        stash(0);
+    if (t_begin < tiles) {
+        fetch(t_begin * kTileKeys);
+        stash(t_begin & 1);
     }
     __syncthreads();
-    for (uint32_t t = 0; t < tiles; ++t) {
+    for (uint32_t t = t_begin; t < tiles; ++t) {
         const int buf = t & 1;
         const uint32_t k0 = t * KN;
         const bool more = t + 1 < tiles;
@@ -564,6 +649,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     }
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
     if (!q_live) return;
+    if constexpr (kSplit) {
+        write_partial<D, VT>(a, split, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
+        return;
+    }
     const bool zero = !__builtin_isfinite(m);
     const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
     const float nan = __builtin_nanf("");
@@ -621,107 +710,146 @@ hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out
 
 }  // namespace
 
+namespace {
+
+// Flash path choice for a shape: 128-query blocks (4 waves) when that gives
+// at least two blocks per CU, else 64-query blocks; a grid still short of
+// 512 blocks splits each query block's key range over up to 8 blocks (each
+// keeping >= 256 keys), merged by sdpa_combine_kernel.
+struct FlashPlan {
+    bool flash = false;
+    bool wide = false;
+    size_t grid = 0;       // blocks before splitting
+    uint32_t splits = 1;
+};
+
+FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned) {
+    FlashPlan p;
+    const uint64_t lim = 0x7fffffffull;
+    if (!aligned || sh.head_dim != sh.value_dim || (sh.head_dim != 64 && sh.head_dim != 128) ||
+        !sh.batch || !sh.q_heads || !sh.kv_heads || sh.q_heads % sh.kv_heads != 0 ||
+        !sh.q_len || sh.q_len > lim || !sh.kv_len || sh.kv_len > lim ||
+        sh.batch * sh.q_heads * ((sh.q_len + 63) / 64) > lim / 8)
+        return p;
+    p.flash = true;
+    const size_t bhs = sh.batch * sh.q_heads;
+    p.wide = ((sh.q_len + 127) / 128) * bhs >= 512;
+    p.grid = ((sh.q_len + (p.wide ? 127 : 63)) / (p.wide ? 128 : 64)) * bhs;
+    if (!p.wide) {
+        size_t want = (512 + p.grid - 1) / p.grid;
+        const size_t by_keys = sh.kv_len / 256;
+        want = want < by_keys ? want : by_keys;
+        p.splits = (uint32_t)(want < 1 ? 1 : want > 8 ? 8 : want);
+    }
+    return p;
+}
+
+size_t partial_bytes(const k::SdpaShape &sh, uint32_t splits) {
+    const size_t rows = sh.batch * sh.q_heads * sh.q_len;
+    return (size_t)splits * rows * (sh.head_dim + 4) * sizeof(float);
+}
+
+// Arguments of the flash kernels; the split buffers are bound when the plan
+// splits and the caller's workspace holds them (otherwise no split).
+SdpaArgs flash_args(const FlashPlan &p, const k::SdpaShape &sh, float scale, bool causal,
+                    void *workspace, size_t workspace_bytes) {
+    SdpaArgs a{};
+    a.batch = (uint32_t)sh.batch;
+    a.qh = (uint32_t)sh.q_heads;
+    a.kvh = (uint32_t)sh.kv_heads;
+    a.group = (uint32_t)(sh.q_heads / sh.kv_heads);
+    a.ql = (uint32_t)sh.q_len;
+    a.kl = (uint32_t)sh.kv_len;
+    a.dim = a.vdim = (uint32_t)sh.head_dim;
+    a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
+    a.scale = scale;
+    a.causal = causal ? 1 : 0;
+    a.splits = 1;
+    if (p.splits > 1 && workspace != nullptr &&
+        workspace_bytes >= partial_bytes(sh, p.splits)) {
+        const size_t rows = sh.batch * sh.q_heads * sh.q_len;
+        a.splits = p.splits;
+        a.part_o = static_cast<float *>(workspace);
+        a.part_ml = reinterpret_cast<f32x4 *>(a.part_o + (size_t)p.splits * rows * sh.head_dim);
+    }
+    return a;
+}
+
+template <typename S>
+hipError_t combine_splits(const SdpaArgs &a, S *out, hipStream_t s) {
+    const size_t n = (size_t)a.batch * a.qh * a.ql * (a.dim / 4);
+    hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2>),
+                       dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, a, out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// One flash launch for the plan's (D, BM) with the mask / split variant.
+#define ICSDK_FLASH_VARIANTS(KERNEL, D, BM, Q, K, V, M, O)                                         \
+    do {                                                                                           \
+        if ((M) != nullptr && split)                                                               \
+            hipLaunchKernelGGL((KERNEL<D, BM, true, true>), grid, block, 0, s, Q, K, V, M, O, a);  \
+        else if ((M) != nullptr)                                                                   \
+            hipLaunchKernelGGL((KERNEL<D, BM, true, false>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else if (split)                                                                            \
+            hipLaunchKernelGGL((KERNEL<D, BM, false, true>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else                                                                                       \
+            hipLaunchKernelGGL((KERNEL<D, BM, false, false>), grid, block, 0, s, Q, K, V, M, O, a);\
+    } while (0)
+#define ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O)                                                  \
+    do {                                                                                           \
+        if (shape.head_dim == 64) {                                                                \
+            if (plan.wide) ICSDK_FLASH_VARIANTS(KERNEL, 64, 128, Q, K, V, M, O);                   \
+            else ICSDK_FLASH_VARIANTS(KERNEL, 64, 64, Q, K, V, M, O);                              \
+        } else {                                                                                   \
+            if (plan.wide) ICSDK_FLASH_VARIANTS(KERNEL, 128, 128, Q, K, V, M, O);                  \
+            else ICSDK_FLASH_VARIANTS(KERNEL, 128, 64, Q, K, V, M, O);                             \
+        }                                                                                          \
+    } while (0)
+
 namespace k {
+
+size_t sdpa_workspace_bytes(const SdpaShape &shape) {
+    const FlashPlan p = flash_plan(shape, true);
+    return p.flash && p.splits > 1 ? partial_bytes(shape, p.splits) : 0;
+}
 
 hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
                     float *out, const SdpaShape &shape, float scale, bool causal,
-                    hipStream_t s) {
+                    void *workspace, size_t workspace_bytes, hipStream_t s) {
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const uint64_t lim = 0x7fffffffull;
-    if (aligned && shape.head_dim == shape.value_dim &&
-        (shape.head_dim == 64 || shape.head_dim == 128) && shape.batch && shape.q_heads &&
-        shape.kv_heads && shape.q_heads % shape.kv_heads == 0 && shape.q_len &&
-        shape.q_len <= lim && shape.kv_len && shape.kv_len <= lim &&
-        shape.batch * shape.q_heads * ((shape.q_len + 63) / 64) <= 0x7fffffffull) {
-        SdpaArgs a{};
-        a.batch = (uint32_t)shape.batch;
-        a.qh = (uint32_t)shape.q_heads;
-        a.kvh = (uint32_t)shape.kv_heads;
-        a.group = (uint32_t)(shape.q_heads / shape.kv_heads);
-        a.ql = (uint32_t)shape.q_len;
-        a.kl = (uint32_t)shape.kv_len;
-        a.dim = a.vdim = (uint32_t)shape.head_dim;
-        a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
-        a.scale = scale;
-        a.causal = causal ? 1 : 0;
-        const size_t bhs = shape.batch * shape.q_heads;
-        const bool wide = ((shape.q_len + 127) / 128) * bhs >= 512;
-        const size_t gx = (shape.q_len + (wide ? 127 : 63)) / (wide ? 128 : 64);
-        const dim3 grid((unsigned)(gx * bhs)), block(wide ? 256 : 128);
-#define ICSDK_FLASH32(D, BM)                                                                      \
-    do {                                                                                          \
-        if (mask)                                                                                 \
-            hipLaunchKernelGGL((sdpa_flash_f32_kernel<D, BM, true>), grid, block, 0, s, q, k, v,    \
-                               mask, out, a);                                                     \
-        else                                                                                      \
-            hipLaunchKernelGGL((sdpa_flash_f32_kernel<D, BM, false>), grid, block, 0, s, q, k, v,   \
-                               mask, out, a);                                                     \
-    } while (0)
-        if (shape.head_dim == 64) {
-            if (wide) ICSDK_FLASH32(64, 128);
-            else ICSDK_FLASH32(64, 64);
-        } else {
-            if (wide) ICSDK_FLASH32(128, 128);
-            else ICSDK_FLASH32(128, 64);
-        }
-#undef ICSDK_FLASH32
-        return hipGetLastError();
-    }
-    return launch_sdpa<float>(q, k, v, mask, out, shape, scale, causal, s);
+    const FlashPlan plan = flash_plan(shape, aligned);
+    if (!plan.flash) return launch_sdpa<float>(q, k, v, mask, out, shape, scale, causal, s);
+    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
+    const bool split = a.splits > 1;
+    const dim3 grid((unsigned)(plan.grid * a.splits)), block(plan.wide ? 256 : 128);
+    ICSDK_FLASH_SHAPES(sdpa_flash_f32_kernel, q, k, v, mask, out);
+    const hipError_t status = hipGetLastError();
+    return status != hipSuccess || !split ? status : combine_splits(a, out, s);
 }
 
 hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                     const uint16_t *mask, uint16_t *out, const SdpaShape &shape, float scale,
-                    bool causal, hipStream_t s) {
+                    bool causal, void *workspace, size_t workspace_bytes, hipStream_t s) {
     auto h = [](const uint16_t *p) { return reinterpret_cast<const _Float16 *>(p); };
+    _Float16 *o16 = reinterpret_cast<_Float16 *>(out);
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const uint64_t lim = 0x7fffffffull;
-    if (aligned && shape.head_dim == shape.value_dim &&
-        (shape.head_dim == 64 || shape.head_dim == 128) && shape.batch && shape.q_heads &&
-        shape.kv_heads && shape.q_heads % shape.kv_heads == 0 && shape.q_len &&
-        shape.q_len <= lim && shape.kv_len && shape.kv_len <= lim &&
-        shape.batch * shape.q_heads * ((shape.q_len + 63) / 64) <= 0x7fffffffull) {
-        SdpaArgs a{};
-        a.batch = (uint32_t)shape.batch;
-        a.qh = (uint32_t)shape.q_heads;
-        a.kvh = (uint32_t)shape.kv_heads;
-        a.group = (uint32_t)(shape.q_heads / shape.kv_heads);
-        a.ql = (uint32_t)shape.q_len;
-        a.kl = (uint32_t)shape.kv_len;
-        a.dim = a.vdim = (uint32_t)shape.head_dim;
-        a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
-        a.scale = scale;
-        a.causal = causal ? 1 : 0;
-        // 128-query blocks (4 waves) when that still gives two blocks per CU,
-        // else 64-query blocks (2 waves) for more of them
-        const size_t bhs = shape.batch * shape.q_heads;
-        const bool wide = ((shape.q_len + 127) / 128) * bhs >= 512;
-        const size_t gx = (shape.q_len + (wide ? 127 : 63)) / (wide ? 128 : 64);
-        const dim3 grid((unsigned)(gx * bhs)), block(wide ? 256 : 128);
-        const _Float16 *m16 = h(mask);
-        _Float16 *o16 = reinterpret_cast<_Float16 *>(out);
-#define ICSDK_FLASH(D, BM)                                                                        \
-    do {                                                                                          \
-        if (mask)                                                                                 \
-            hipLaunchKernelGGL((sdpa_flash_kernel<D, BM, true>), grid, block, 0, s, h(q), h(k),     \
-                               h(v), m16, o16, a);                                                \
-        else                                                                                      \
-            hipLaunchKernelGGL((sdpa_flash_kernel<D, BM, false>), grid, block, 0, s, h(q), h(k),    \
-                               h(v), m16, o16, a);                                                \
-    } while (0)
-        if (shape.head_dim == 64) {
-            if (wide) ICSDK_FLASH(64, 128);
-            else ICSDK_FLASH(64, 64);
-        } else {
-            if (wide) ICSDK_FLASH(128, 128);
-            else ICSDK_FLASH(128, 64);
-        }
-#undef ICSDK_FLASH
-        return hipGetLastError();
-    }
-    return launch_sdpa<_Float16>(h(q), h(k), h(v), h(mask), reinterpret_cast<_Float16 *>(out),
-                                 shape, scale, causal, s);
+    const FlashPlan plan = flash_plan(shape, aligned);
+    if (!plan.flash)
+        return launch_sdpa<_Float16>(h(q), h(k), h(v), h(mask), o16, shape, scale, causal, s);
+    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
+    const bool split = a.splits > 1;
+    const dim3 grid((unsigned)(plan.grid * a.splits)), block(plan.wide ? 256 : 128);
+    ICSDK_FLASH_SHAPES(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
+    const hipError_t status = hipGetLastError();
+    return status != hipSuccess || !split ? status : combine_splits(a, o16, s);
 }
 
 }  // namespace k
+
+#undef ICSDK_FLASH_SHAPES
+#undef ICSDK_FLASH_VARIANTS
+
+
 }  // namespace icsdk

@@ -112,12 +112,16 @@ hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t
 struct SdpaShape {
     size_t batch, q_heads, kv_heads, q_len, kv_len, head_dim, value_dim;
 };
+// `workspace` (may be null) lets a small grid split each query block's key
+// range over several blocks: sdpa_workspace_bytes(shape) bytes, 0 when the
+// shape would not split.
+size_t sdpa_workspace_bytes(const SdpaShape &shape);
 hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
                     float *out, const SdpaShape &shape, float scale, bool causal,
-                    hipStream_t s);
+                    void *workspace, size_t workspace_bytes, hipStream_t s);
 hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                     const uint16_t *mask, uint16_t *out, const SdpaShape &shape, float scale,
-                    bool causal, hipStream_t s);
+                    bool causal, void *workspace, size_t workspace_bytes, hipStream_t s);
 
 // Quantized linear y[rows, out] = x[rows, in] * dequant(w)^T with w packed
 // [out, in/32, 34] (Q8_0) or [out, in/32, 18] (Q4_0); in % 32 == 0.

@@ -61,15 +61,19 @@ private:
     uint32_t *word_;
 };
 
-// A pool block held for the duration of one call. Returning it to the pool
-// right after the launches is safe: every later user of the block enqueues
-// on the same SDK stream, after this call's kernels.
+// A pool block held for the duration of one call (none for zero bytes).
+// Returning it to the pool right after the launches is safe: every later
+// user of the block enqueues on the same SDK stream, after this call's
+// kernels.
 class ScratchBlock {
 public:
-    explicit ScratchBlock(size_t bytes) : bytes_(bytes == 0 ? 1 : bytes), ptr_(scratch_acquire(bytes_)) {}
+    explicit ScratchBlock(size_t bytes)
+        : bytes_(bytes), ptr_(bytes == 0 ? nullptr : scratch_acquire(bytes)) {}
     ScratchBlock(const ScratchBlock &) = delete;
     ScratchBlock &operator=(const ScratchBlock &) = delete;
-    ~ScratchBlock() { scratch_release(ptr_, bytes_); }
+    ~ScratchBlock() {
+        if (ptr_ != nullptr) scratch_release(ptr_, bytes_);
+    }
     void *get() const { return ptr_; }
 
 private:

@@ -31,6 +31,8 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (1, 4, 1, 300, 300, 128, 128),  # MFMA path: ragged query and key tiles, 4 heads per kv head
     (1, 2, 2, 129, 1000, 64, 64),   # MFMA path: kv longer than q (causal offset 871)
     (3, 2, 2, 1, 77, 128, 128),     # MFMA path: one query
+    (1, 2, 1, 40, 2048, 128, 128),  # MFMA path, key range split over 8 blocks
+    (2, 3, 3, 100, 1500, 64, 64),   # MFMA path, 5 splits of uneven tile counts
 ]
 
 
@@ -182,3 +184,29 @@ def test_device_sdpa_validation(sdk):
     wide = sdk.tensor("f16", (1, 1, 2, 520))
     ok, msg = sdk.try_call("tensor_sdpa_device_f16", wide, wide, wide, None, 1.0, 0, wide)
     assert not ok and "up to 512" in msg
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_split_key_range_special_rows(sdk, orc, dtype):
+    """A small grid with a long key range is split over several blocks and
+    merged; the special-row rules hold across splits, bitwise vs the oracle:
+    row 0 sees one key, in the last split; row 1 has a NaN query (every score
+    NaN: nothing visible, zero row); row 2 has a +inf mask entry in one split
+    (row max +inf: zero row); row 3 is ordinary."""
+    npt = np.float16 if dtype == "f16" else np.float32
+    lq, lk, d = 4, 1024, 64
+    q = orc.normal((1, 1, lq, d), 33, 0, 0.0, 1.0, dtype)
+    k = orc.normal((1, 1, lk, d), 33, 1, 0.0, 1.0, dtype)
+    v = orc.normal((1, 1, lk, d), 33, 2, 0.0, 1.0, dtype)
+    q[0, 0, 1, 5] = np.nan
+    mask = np.zeros((lq, lk), npt)
+    mask[0, :] = -np.inf
+    mask[0, 900] = 0
+    mask[2, 500] = np.inf
+    got = run_device(sdk, q, k, v, mask, 0.125, False, dtype)
+    want = orc.sdpa(q, k, v, mask, 0.125, False)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert (got[0, 0, 1] == 0).all() and (got[0, 0, 2] == 0).all()
+    np.testing.assert_array_equal(got[0, 0, 0], v[0, 0, 900].astype(got.dtype))
+    weight = orc.sdpa_abs_weight(q, k, v, mask, 0.125, False)
+    check(got[0, 0, 3:], want[0, 0, 3:], weight[0, 0, 3:], dtype, "ordinary row")
