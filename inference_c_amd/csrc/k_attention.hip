@@ -184,6 +184,8 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 // and V^T is stored with that key order (slot 16c + 8h + i), so each A
 // fragment is one 16-byte LDS read.
 constexpr int kFlashN = 64;    // keys per tile
+// s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt at their no-wait maxima)
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // Block order. MI355X dispatches a launch's workgroups to its 8 XCDs
 // round-robin (block b on XCD b % 8) and each XCD has its own 4 MB L2. The
@@ -305,6 +307,12 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
 #pragma unroll
         for (int c = 0; c < KC; ++c) qf[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
     }
+    // wait for Q here: otherwise the wait analysis of the tile loop cannot
+    // tell these loads from the next tile's prefetch and makes every S^T MFMA
+    // wait for one more of the prefetch loads
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __builtin_amdgcn_sched_barrier(0);
     float16v o[VT];
 #pragma unroll
     for (int t = 0; t < VT; ++t)
@@ -529,6 +537,9 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
             qf[4 * c + 3] = t.w;
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);   // Q ready before the tile loop
+    __builtin_amdgcn_sched_barrier(0);
     float16v o[VT];
 #pragma unroll
     for (int t = 0; t < VT; ++t)
@@ -714,8 +725,11 @@ namespace {
 
 // Flash path choice for a shape: 128-query blocks (4 waves) when that gives
 // at least two blocks per CU, else 64-query blocks; a grid still short of
-// 512 blocks splits each query block's key range over up to 8 blocks (each
-// keeping >= 256 keys), merged by sdpa_combine_kernel.
+// that splits each query block's key range over up to 8 blocks, merged by
+// sdpa_combine_kernel: toward 2 blocks per CU with >= 256 keys per split for
+// f16 (a 64-key tile is cheap, so a split must amortise its fixed cost), and
+// toward 4 blocks per CU with >= 128 keys for f32 (32-key tiles of 64
+// MFMAs each). Measured on the 12 x 1024 x 1024 x 64 shape.
 struct FlashPlan {
     bool flash = false;
     bool wide = false;
@@ -723,7 +737,7 @@ struct FlashPlan {
     uint32_t splits = 1;
 };
 
-FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned) {
+FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32) {
     FlashPlan p;
     const uint64_t lim = 0x7fffffffull;
     if (!aligned || sh.head_dim != sh.value_dim || (sh.head_dim != 64 && sh.head_dim != 128) ||
@@ -736,8 +750,9 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned) {
     p.wide = ((sh.q_len + 127) / 128) * bhs >= 512;
     p.grid = ((sh.q_len + (p.wide ? 127 : 63)) / (p.wide ? 128 : 64)) * bhs;
     if (!p.wide) {
-        size_t want = (512 + p.grid - 1) / p.grid;
-        const size_t by_keys = sh.kv_len / 256;
+        const size_t target = f32 ? 1024 : 512;
+        size_t want = (target + p.grid - 1) / p.grid;
+        const size_t by_keys = sh.kv_len / (f32 ? 128 : 256);
         want = want < by_keys ? want : by_keys;
         p.splits = (uint32_t)(want < 1 ? 1 : want > 8 ? 8 : want);
     }
@@ -810,8 +825,8 @@ hipError_t combine_splits(const SdpaArgs &a, S *out, hipStream_t s) {
 
 namespace k {
 
-size_t sdpa_workspace_bytes(const SdpaShape &shape) {
-    const FlashPlan p = flash_plan(shape, true);
+size_t sdpa_workspace_bytes(const SdpaShape &shape, bool f32) {
+    const FlashPlan p = flash_plan(shape, true, f32);
     return p.flash && p.splits > 1 ? partial_bytes(shape, p.splits) : 0;
 }
 
@@ -819,7 +834,7 @@ hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float 
                     float *out, const SdpaShape &shape, float scale, bool causal,
                     void *workspace, size_t workspace_bytes, hipStream_t s) {
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const FlashPlan plan = flash_plan(shape, aligned);
+    const FlashPlan plan = flash_plan(shape, aligned, true);
     if (!plan.flash) return launch_sdpa<float>(q, k, v, mask, out, shape, scale, causal, s);
     const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
     const bool split = a.splits > 1;
@@ -835,7 +850,7 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     auto h = [](const uint16_t *p) { return reinterpret_cast<const _Float16 *>(p); };
     _Float16 *o16 = reinterpret_cast<_Float16 *>(out);
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const FlashPlan plan = flash_plan(shape, aligned);
+    const FlashPlan plan = flash_plan(shape, aligned, false);
     if (!plan.flash)
         return launch_sdpa<_Float16>(h(q), h(k), h(v), h(mask), o16, shape, scale, causal, s);
     const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
