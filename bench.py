@@ -427,6 +427,34 @@ def pmc_probe(sdk, reps=3):
     del packed
     ops.append(("linear_q8_0_f16_1x8192_to_28672",
                 lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
+    # kernels that stage data in LDS, for the LDS instruction / bank-conflict
+    # pass: RoPE (angle table), a [4096, 4096] f16 transpose (64x64 tiles),
+    # the global sum/max (cross-wave combine) and flash attention f16 / f32
+    t["q5"], t["k5"] = sdk.tensor("f16", (4096, 32, 64)), sdk.tensor("f16", (4096, 32, 64))
+    sdk.call("tensor_fill_normal", t["q5"], 5, 2, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["k5"], 5, 3, 0.0, 1.0)
+    ops.append(("rope_f16", lambda: sdk.call("tensor_rope_f16", t["q5"], t["k5"], 32, 32, 64,
+                                             10000.0, 0)))
+    t["xt"], t["yt"] = sdk.tensor("f16", (4096, 4096)), sdk.tensor("f16", (4096, 4096))
+    sdk.call("tensor_fill_normal", t["xt"], 4, 0, 0.0, 1.0)
+    transpose = TensorView.make((4096, 4096), (1, 4096), 0)
+    ops.append(("transpose_f16", lambda: sdk.call("tensor_view_add_mul_f16", t["xt"], transpose,
+                                                  None, None, t["yt"])))
+    t["g"] = sdk.tensor("f32", (1 << 28,))
+    t["gs"], t["gm"] = sdk.tensor("f64", (1,)), sdk.tensor("f32", (1,))
+    sdk.call("tensor_fill_uniform", t["g"], 0, 5, -1.0, 1.0)
+    ops.append(("global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", t["g"], t["gs"],
+                                                       t["gm"])))
+    for dtype in ("f16", "f32"):
+        qa = sdk.tensor(dtype, (1, 32, 2048, 128))
+        ka, va = sdk.tensor(dtype, (1, 8, 2048, 128)), sdk.tensor(dtype, (1, 8, 2048, 128))
+        oa = sdk.tensor(dtype, (1, 32, 2048, 128))
+        for i, x in enumerate((qa, ka, va)):
+            sdk.call("tensor_fill_normal", x, 6, i, 0.0, 1.0)
+        t["attn_" + dtype] = (qa, ka, va, oa)
+        ops.append((f"sdpa_{dtype}_prefill", lambda d=dtype: sdk.call(
+            f"tensor_sdpa_device_{d}", *t["attn_" + d][:3], None, 0.08838834764831845, 1,
+            t["attn_" + d][3])))
     for name, fn in ops:
         for _ in range(reps):
             sdk.call("tensor_fill_uniform", flush, 7, 0, -1.0, 1.0)
