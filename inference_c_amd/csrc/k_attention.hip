@@ -393,22 +393,35 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                         &ks[buf][(32 * hblk + col) * KROW + 16 * c + 8 * half]);
                     st[hblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], st[hblk], 0, 0, 0);
                 }
-#pragma unroll
-            for (int hblk = 0; hblk < 2; ++hblk) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t kk = k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4;
-                    // scores are kept in log2 units: s * log2(e)
-                    float s = st[hblk][r] * scale2;
-                    if constexpr (kMask) {
-                        if (kk < a.kl && q_live)
-                            s = __builtin_fmaf((float)mask[(size_t)qi * a.kl + kk], kLog2e, s);
-                    }
-                    if (!interior && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
-                        s = neg_inf;
-                    st[hblk][r] = s;
-                    local_max = fmaxf(local_max, s);
+            // scores are kept in log2 units: s * log2(e); the interior test is
+            // taken once per tile (inside the unrolled loop it became one
+            // branch per score)
+            auto score = [&](float raw, uint32_t kk, bool edge) {
+                float s = raw * scale2;
+                if constexpr (kMask) {
+                    if (kk < a.kl && q_live)
+                        s = __builtin_fmaf((float)mask[(size_t)qi * a.kl + kk], kLog2e, s);
                 }
+                if (edge && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
+                    s = neg_inf;
+                return s;
+            };
+            if (interior) {
+#pragma unroll
+                for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, false);
+                        local_max = fmaxf(local_max, st[hblk][r]);
+                    }
+            } else {
+#pragma unroll
+                for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, true);
+                        local_max = fmaxf(local_max, st[hblk][r]);
+                    }
             }
             const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
             const bool none = m_new == neg_inf;   // nothing visible to this query yet
@@ -611,17 +624,27 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
             }
             float st[16];
             float local_max = neg_inf;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t kk = k0 + 8 * (r / 4) + 4 * half + r % 4;
-                float s = (acc[0][r] + acc[1][r]) * a.scale;
+            auto score = [&](float raw, uint32_t kk, bool edge) {
+                float s = raw * a.scale;
                 if constexpr (kMask) {
                     if (kk < a.kl && q_live) s = s + mask[(size_t)qi * a.kl + kk];
                 }
-                if (!interior && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
+                if (edge && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
                     s = neg_inf;
-                st[r] = s;
-                local_max = fmaxf(local_max, s);
+                return s;
+            };
+            if (interior) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    st[r] = score(acc[0][r] + acc[1][r], k0 + 8 * (r / 4) + 4 * half + r % 4, false);
+                    local_max = fmaxf(local_max, st[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    st[r] = score(acc[0][r] + acc[1][r], k0 + 8 * (r / 4) + 4 * half + r % 4, true);
+                    local_max = fmaxf(local_max, st[r]);
+                }
             }
             const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
             const bool none = m_new == neg_inf;
