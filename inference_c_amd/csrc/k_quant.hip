@@ -359,7 +359,7 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
             done = left;
         } else {
             done = left < kMaxGroups * 8 ? left : kMaxGroups * 8;
-            status = launch_gemv<kQ8, 8, 2>(xr, w, yr, done, in, out, s);
+            status = launch_gemv<kQ8, 8, 4>(xr, w, yr, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;
