@@ -199,6 +199,51 @@ __device__ inline uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
     return xcd * q + (xcd < r ? xcd : r) + j;
 }
 
+// Max and sum of a value over the lane pair (l, l ^ 32). v_permlane32_swap
+// with both operands v leaves every lane holding its own value in one result
+// and its partner's in the other (lanes 0-31 keep r0 and receive lane + 32 in
+// r1; lanes 32-63 receive lane - 32 in r0 and keep r1), so one cross-lane
+// VALU op replaces a round trip through LDS (ds_bpermute).
+// The two halves of the wave swap values with v_permlane32_swap: each lane
+// gets back its own value and the one of lane +-32. The vector's elements
+// are copied into scalars before the bit cast (a bit cast of an element of
+// the returned vector reads element 0).
+__device__ inline float pair_value(float v, float &partner) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const unsigned lo = r[0], hi = r[1];
+    partner = __builtin_bit_cast(float, hi);
+    return __builtin_bit_cast(float, lo);
+}
+__device__ inline float pair_max(float v) {
+    float b;
+    const float a = pair_value(v, b);
+    return fmaxf(a, b);
+}
+__device__ inline float pair_sum(float v) {
+    float b;
+    const float a = pair_value(v, b);
+    return a + b;
+}
+
+// Scheduling of an unrolled chain of N (LDS read, MFMA) pairs: the first
+// kAhead reads, then one MFMA and one read alternately, then the last MFMAs.
+// Each MFMA then consumes a fragment read kAhead MFMAs earlier (~128
+// cycles), which covers the LDS latency; left to itself the scheduler reads
+// one fragment ahead and every MFMA waits for its read.
+template <int N>
+__device__ inline void lds_read_ahead() {
+    constexpr int kAhead = 4;
+    constexpr int kMfma = 0x008, kDsRead = 0x100;
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
+#pragma unroll
+    for (int i = 0; i < N - kAhead; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
+}
+
 __device__ inline uint32_t vt_slot(uint32_t key) {
     const uint32_t within = key % 16;
     return (key / 16) * 16 + 8 * ((within / 4) % 2) + (within / 8) * 4 + within % 4;
@@ -393,6 +438,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                         &ks[buf][(32 * hblk + col) * KROW + 16 * c + 8 * half]);
                     st[hblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], st[hblk], 0, 0, 0);
                 }
+            lds_read_ahead<2 * KC>();
             // scores are kept in log2 units: s * log2(e); the interior test is
             // taken once per tile (inside the unrolled loop it became one
             // branch per score)
@@ -406,13 +452,15 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                     s = neg_inf;
                 return s;
             };
+            // four independent max chains instead of one of 32
+            float part_max[4] = {neg_inf, neg_inf, neg_inf, neg_inf};
             if (interior) {
 #pragma unroll
                 for (int hblk = 0; hblk < 2; ++hblk)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, false);
-                        local_max = fmaxf(local_max, st[hblk][r]);
+                        part_max[r % 4] = fmaxf(part_max[r % 4], st[hblk][r]);
                     }
             } else {
 #pragma unroll
@@ -420,10 +468,11 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, true);
-                        local_max = fmaxf(local_max, st[hblk][r]);
+                        part_max[r % 4] = fmaxf(part_max[r % 4], st[hblk][r]);
                     }
             }
-            const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
+            local_max = fmaxf(fmaxf(part_max[0], part_max[1]), fmaxf(part_max[2], part_max[3]));
+            const float m_new = fmaxf(m, pair_max(local_max));
             const bool none = m_new == neg_inf;   // nothing visible to this query yet
             if (wave_any(none)) {
                 // a NaN score is dropped while nothing is visible; remember it
@@ -435,14 +484,15 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
             }
             const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
             half8 pf[4];
-            float local_sum = 0.0f;
+            float part_sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < 32; ++r) {
                 const float p = none ? 0.0f : __builtin_amdgcn_exp2f(st[r / 16][r % 16] - m_new);
-                local_sum += p;
+                part_sum[r % 4] += p;
                 pf[r / 8][r % 8] = (_Float16)p;
             }
-            l = l * alpha + (local_sum + __shfl_xor(local_sum, 32, kWave));
+            const float local_sum = (part_sum[0] + part_sum[1]) + (part_sum[2] + part_sum[3]);
+            l = l * alpha + pair_sum(local_sum);
             m = m_new;
             const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
             if (rescale) {
@@ -460,6 +510,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                         &vs[buf][(32 * tt + col) * VROW + 16 * c + 8 * half]);
                     o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[tt], 0, 0, 0);
                 }
+            lds_read_ahead<4 * VT>();
         }
         if (more) stash(buf ^ 1);
         __syncthreads();
@@ -633,20 +684,22 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
                     s = neg_inf;
                 return s;
             };
+            float part_max[4] = {neg_inf, neg_inf, neg_inf, neg_inf};
             if (interior) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     st[r] = score(acc[0][r] + acc[1][r], k0 + 8 * (r / 4) + 4 * half + r % 4, false);
-                    local_max = fmaxf(local_max, st[r]);
+                    part_max[r % 4] = fmaxf(part_max[r % 4], st[r]);
                 }
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     st[r] = score(acc[0][r] + acc[1][r], k0 + 8 * (r / 4) + 4 * half + r % 4, true);
-                    local_max = fmaxf(local_max, st[r]);
+                    part_max[r % 4] = fmaxf(part_max[r % 4], st[r]);
                 }
             }
-            const float m_new = fmaxf(m, fmaxf(local_max, __shfl_xor(local_max, 32, kWave)));
+            local_max = fmaxf(fmaxf(part_max[0], part_max[1]), fmaxf(part_max[2], part_max[3]));
+            const float m_new = fmaxf(m, pair_max(local_max));
             const bool none = m_new == neg_inf;
             if (wave_any(none)) {
                 bool local_nan = false;
@@ -655,13 +708,14 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
                 nan_seen = nan_seen || (none && local_nan);
             }
             const float alpha = none ? 1.0f : expf(m - m_new);
-            float local_sum = 0.0f;
+            float part_sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 st[r] = none ? 0.0f : expf(st[r] - m_new);
-                local_sum += st[r];
+                part_sum[r % 4] += st[r];
             }
-            l = l * alpha + (local_sum + __shfl_xor(local_sum, 32, kWave));
+            const float local_sum = (part_sum[0] + part_sum[1]) + (part_sum[2] + part_sum[3]);
+            l = l * alpha + pair_sum(local_sum);
             m = m_new;
             if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
