@@ -79,20 +79,27 @@ __device__ inline float block_dot(const uint32_t (&q)[Fmt<kQ8>::kWords], const u
             s1 = __builtin_amdgcn_fdot2(hi, as_half2(x[2 * j + 1]), s1, false);
         }
     } else {
+        // byte b of the word into the low byte of a half with 0x64 above it:
+        // 0x64bb = 1024 + lo + 16 hi. Masking keeps 1024 + lo (0x640n) or
+        // 1024 + 16 hi (0x64n0); the packed subtract leaves lo - 8 and
+        // 16 (hi - 8), both exact in f16. The high-nibble products go to
+        // their own sums, scaled by 1/16 (exact) at the end.
+        const half2_t bias16 = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 16 * 8
+        float h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            // bytes 4j, 4j+1 and 4j+2, 4j+3 spread to the low byte of each half
-            const uint32_t p01 = __builtin_amdgcn_perm(0u, q[j], 0x0c010c00u);
-            const uint32_t p23 = __builtin_amdgcn_perm(0u, q[j], 0x0c030c02u);
-            const half2_t w01 = as_half2((p01 & 0x000f000fu) | 0x64006400u) - bias4;
-            const half2_t w23 = as_half2((p23 & 0x000f000fu) | 0x64006400u) - bias4;
-            const half2_t w1617 = as_half2(((p01 >> 4) & 0x000f000fu) | 0x64006400u) - bias4;
-            const half2_t w1819 = as_half2(((p23 >> 4) & 0x000f000fu) | 0x64006400u) - bias4;
+            const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, q[j], 0x04010400u);
+            const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, q[j], 0x04030402u);
+            const half2_t w01 = as_half2(p01 & 0xff0fff0fu) - bias4;
+            const half2_t w23 = as_half2(p23 & 0xff0fff0fu) - bias4;
+            const half2_t w1617 = as_half2(p01 & 0xfff0fff0u) - bias16;
+            const half2_t w1819 = as_half2(p23 & 0xfff0fff0u) - bias16;
             s0 = __builtin_amdgcn_fdot2(w01, as_half2(x[2 * j]), s0, false);
             s1 = __builtin_amdgcn_fdot2(w23, as_half2(x[2 * j + 1]), s1, false);
-            s0 = __builtin_amdgcn_fdot2(w1617, as_half2(x[8 + 2 * j]), s0, false);
-            s1 = __builtin_amdgcn_fdot2(w1819, as_half2(x[8 + 2 * j + 1]), s1, false);
+            h0 = __builtin_amdgcn_fdot2(w1617, as_half2(x[8 + 2 * j]), h0, false);
+            h1 = __builtin_amdgcn_fdot2(w1819, as_half2(x[8 + 2 * j + 1]), h1, false);
         }
+        return (s0 + s1) + (h0 + h1) * 0.0625f;
     }
     return s0 + s1;
 }
