@@ -73,7 +73,7 @@ int host_run(const T *q, const T *k, const T *v, const T *mask, T *out, size_t b
     const void *pm = mask ? st.in(mask, c.mask * sizeof(T)) : nullptr;
     void *po = st.out(out, c.out * sizeof(T));
     if (st.failed()) return 0;
-    const size_t ws_want = k::sdpa_workspace_bytes(shape, sizeof(T) == 4);
+    const size_t ws_want = k::sdpa_workspace_bytes(shape, sizeof(T) == 4, causal != 0);
     ScratchBlock workspace(ws_want);
     const size_t ws_bytes = workspace.get() ? ws_want : 0;
     hipError_t status;
@@ -169,7 +169,7 @@ int sdpa_device(TensorDType dtype, const TensorBuffer *q, const TensorBuffer *k,
     };
     // split-key partials live in a pool block, returned right after the
     // launches (later users of the block enqueue behind them on the stream)
-    const size_t ws_want = k::sdpa_workspace_bytes(shape, dtype == TENSOR_DTYPE_F32);
+    const size_t ws_want = k::sdpa_workspace_bytes(shape, dtype == TENSOR_DTYPE_F32, causal != 0);
     ScratchBlock workspace(ws_want);
     const size_t ws_bytes = workspace.get() ? ws_want : 0;
     const hipError_t status =

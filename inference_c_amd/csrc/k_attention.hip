@@ -21,10 +21,13 @@
 // reorders the roundings of p; outputs therefore agree with the reference to
 // a few roundings of sum_j p_j |v_j|.
 #include "kern_common.hpp"
+#include <algorithm>
 #include "kernels.hpp"
 
 namespace icsdk {
 namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxRowRegs = 8;  // D, Dv <= 8 * 64
 
@@ -34,13 +37,46 @@ struct SdpaArgs {
     uint32_t causal_offset;           // kl > ql ? kl - ql : 0
     float scale;
     int causal;
-    // split key range (flash kernels): `splits` blocks share one query block,
-    // each writes its unnormalised output rows to part_o[split][row][D] and
-    // {running max, sum, NaN flag, 0} to part_ml[split][row]
-    uint32_t splits;
+    // Flash work schedule. Every (batch, head) has `items` work items; item r
+    // is key-tile part `part` of `parts` of query block `qblock`, packed as
+    // qblock | part << 16 | parts << 24 in item[r] when `table` is set (else
+    // item r is query block qblocks - 1 - r, whole). A query block of n key
+    // tiles has split_parts(n, split_tiles) parts; a part's block writes its
+    // unnormalised output rows to part_o[part][row][D] and {running max, sum,
+    // NaN flag, 0} to part_ml[part][row], merged by sdpa_combine_kernel.
+    uint32_t items, qblocks;
+    uint32_t split_tiles;   // 0: no query block is split
+    uint32_t table;
+    uint32_t xcd_heads;     // keep the q-heads of one kv head on one XCD
     float *part_o;
     f32x4 *part_ml;
+    uint32_t item[128];
 };
+constexpr uint32_t kMaxFlashItems = 128;
+constexpr uint32_t kMaxKeyParts = 8;
+constexpr uint32_t kMinPartTiles = 4;   // a part amortises its set-up and the merge
+
+// Key tiles (of tk keys) that the queries of query block j (bm queries) may
+// see: all kl keys, or when causal those up to its last query + offset.
+__host__ __device__ inline uint32_t flash_tiles(uint32_t ql, uint32_t kl, bool causal,
+                                                uint32_t offset, uint32_t bm, uint32_t tk,
+                                                uint32_t j) {
+    const uint32_t last = j * bm + bm - 1 < ql - 1 ? j * bm + bm - 1 : ql - 1;
+    const uint64_t seen = (uint64_t)last + offset + 1;
+    const uint64_t key_end = causal && seen < kl ? seen : kl;
+    return (uint32_t)((key_end + tk - 1) / tk);
+}
+
+// Parts of a query block of `tiles` key tiles: about tiles / split_tiles,
+// each of at least kMinPartTiles tiles, at most kMaxKeyParts.
+__host__ __device__ inline uint32_t split_parts(uint32_t tiles, uint32_t split_tiles) {
+    if (split_tiles == 0) return 1;
+    uint32_t n = (tiles + split_tiles - 1) / split_tiles;
+    const uint32_t most = tiles / kMinPartTiles;
+    n = n < most ? n : most;
+    n = n < kMaxKeyParts ? n : kMaxKeyParts;
+    return n < 1 ? 1 : n;
+}
 
 __device__ inline float broadcast_lane(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -184,19 +220,41 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 // and V^T is stored with that key order (slot 16c + 8h + i), so each A
 // fragment is one 16-byte LDS read.
 constexpr int kFlashN = 64;    // keys per tile
+constexpr float kLazyLog2 = 8.0f;   // rescale when a row maximum grows by more than 2^8
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt at their no-wait maxima)
 constexpr int kWaitVmcnt0 = 0x0F70;
 
-// Block order. MI355X dispatches a launch's workgroups to its 8 XCDs
-// round-robin (block b on XCD b % 8) and each XCD has its own 4 MB L2. The
-// blocks of one (batch, head) read the same K and V tiles, so the grid is
-// renumbered to give each XCD one contiguous range of (head, query block)
-// pairs: a kv head's K/V then live in one L2 instead of being fetched into
-// all eight. (A bijection on [0, n).)
-__device__ inline uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
-    constexpr uint32_t kXcds = 8;
-    const uint32_t q = n / kXcds, r = n % kXcds, xcd = b % kXcds, j = b / kXcds;
-    return xcd * q + (xcd < r ? xcd : r) + j;
+// Block -> work item. Blocks are numbered item-rank-major (all (batch, head)
+// pairs of the largest item first), so the blocks dispatched first are the
+// longest and the short ones fill in behind them. MI355X dispatches a
+// launch's workgroups to its 8 XCDs round-robin (block b on XCD b % 8) and
+// each XCD has its own 4 MB L2: with xcd_heads (batch * kv heads divisible
+// by 8, so b % 8 == p % 8), XCD x takes the q-heads of kv units x, x + 8, ...
+// and a kv head's K/V tiles are fetched into one L2 instead of all eight.
+struct FlashItem {
+    uint32_t bh, qblock, part, parts;
+};
+__device__ inline FlashItem flash_item(const SdpaArgs &a, uint32_t block) {
+    const uint32_t bhs = a.batch * a.qh;
+    const uint32_t r = block / bhs, p = block % bhs;
+    FlashItem it;
+    if (a.xcd_heads) {
+        const uint32_t x = p % 8, i = p / 8;
+        it.bh = (x + 8 * (i / a.group)) * a.group + i % a.group;
+    } else {
+        it.bh = p;
+    }
+    if (a.table) {
+        const uint32_t e = a.item[r];
+        it.qblock = e & 0xffffu;
+        it.part = (e >> 16) & 0xffu;
+        it.parts = e >> 24;
+    } else {
+        it.qblock = a.qblocks - 1 - r;
+        it.part = 0;
+        it.parts = 1;
+    }
+    return it;
 }
 
 // Max and sum of a value over the lane pair (l, l ^ 32). v_permlane32_swap
@@ -244,6 +302,20 @@ __device__ inline void lds_read_ahead() {
     __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
 }
 
+// A wave issuing a chain of MFMAs runs at raised priority, so that the
+// other waves of its SIMD (in their softmax) take the issue cycles between
+// its MFMAs instead of both waves reaching the same phase together.
+__device__ inline void mfma_phase_begin() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);
+}
+__device__ inline void mfma_phase_end() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ inline uint32_t vt_slot(uint32_t key) {
     const uint32_t within = key % 16;
     return (key / 16) * 16 + 8 * ((within / 4) % 2) + (within / 8) * 4 + within % 4;
@@ -267,22 +339,31 @@ __device__ inline void write_partial(const SdpaArgs &a, uint32_t split, size_t r
     if (half == 0) a.part_ml[(size_t)split * rows + row] = f32x4{m, l, nan_seen ? 1.0f : 0.0f, 0.0f};
 }
 
-// Merges the splits of each query row: M = max of the splits' maxima; a row
-// whose M is not finite is zero; a NaN flag with a finite M makes the row
-// NaN; otherwise out = (sum_s w_s o_s) * (1 / sum_s w_s l_s) with
-// w_s = exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per
-// 4 output elements.
+// Merges the parts of each split query row (rows first_row .. ql - 1 of
+// every (batch, head): split query blocks are a suffix, since a later query
+// block never sees fewer keys): M = max of the parts' maxima; a row whose M
+// is not finite is zero; a NaN flag with a finite M makes the row NaN;
+// otherwise out = (sum_s w_s o_s) * (1 / sum_s w_s l_s) with w_s =
+// exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per 4
+// output elements.
 template <typename S, bool kLog2>
-__global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__restrict__ out) {
+__global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__restrict__ out,
+                                                              uint32_t bm, uint32_t tk,
+                                                              uint32_t first_row) {
     const size_t rows = (size_t)a.batch * a.qh * a.ql;
+    const uint32_t suffix = a.ql - first_row;
     const uint32_t groups = a.dim / 4;
     const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= rows * groups) return;
-    const size_t row = i / groups;
+    if (i >= (size_t)a.batch * a.qh * suffix * groups) return;
+    const size_t srow = i / groups;
     const uint32_t g = (uint32_t)(i % groups);
+    const uint32_t qi = first_row + (uint32_t)(srow % suffix);
+    const size_t row = srow / suffix * a.ql + qi;
+    const uint32_t splits = split_parts(
+        flash_tiles(a.ql, a.kl, a.causal != 0, a.causal_offset, bm, tk, qi / bm), a.split_tiles);
     float big = -__builtin_inff();
     bool nan_flag = false;
-    for (uint32_t s = 0; s < a.splits; ++s) {
+    for (uint32_t s = 0; s < splits; ++s) {
         const f32x4 ml = a.part_ml[(size_t)s * rows + row];
         big = fmaxf(big, ml.x);
         nan_flag = nan_flag || ml.z != 0.0f;
@@ -290,7 +371,7 @@ __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__r
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float total = 0.0f;
     if (__builtin_isfinite(big)) {
-        for (uint32_t s = 0; s < a.splits; ++s) {
+        for (uint32_t s = 0; s < splits; ++s) {
             const f32x4 ml = a.part_ml[(size_t)s * rows + row];
             // a split that saw no visible key has sum 0 and output 0; every
             // other split is added even at weight 0, so a NaN it holds stays
@@ -333,12 +414,8 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
     const uint32_t col = lane & 31, half = lane >> 5;
-    const uint32_t qblocks = (a.ql + BM - 1) / BM;
-    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-    const uint32_t split = kSplit ? logical % a.splits : 0;
-    const uint32_t pair = kSplit ? logical / a.splits : logical;
-    const uint32_t qblock = pair % qblocks;
-    const uint32_t bh = pair / qblocks;
+    const FlashItem item = flash_item(a, blockIdx.x);
+    const uint32_t qblock = item.qblock, bh = item.bh;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
     const uint32_t qw = qblock * BM + wave * 32;        // the wave's first query
@@ -368,14 +445,11 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     constexpr float kLog2e = 1.4426950408889634f;
     const float scale2 = a.scale * kLog2e;
 
-    // keys any query of the block can see, and of this wave
-    const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
-    const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
-                                      : (uint64_t)a.kl;
-    const uint32_t all_tiles = (uint32_t)((key_end + kFlashN - 1) / kFlashN);
-    // this block's share of the key tiles (all of them unless split)
-    const uint32_t share = kSplit ? (all_tiles + a.splits - 1) / a.splits : all_tiles;
-    const uint32_t t_begin = min(split * share, all_tiles);
+    // key tiles any query of the block can see; this block's part of them
+    const uint32_t all_tiles = flash_tiles(a.ql, a.kl, a.causal != 0, a.causal_offset, BM,
+                                           kFlashN, qblock);
+    const uint32_t share = (all_tiles + item.parts - 1) / item.parts;
+    const uint32_t t_begin = min(item.part * share, all_tiles);
     const uint32_t tiles = min(t_begin + share, all_tiles);
     const bool wave_live = qw < a.ql;
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
@@ -385,6 +459,17 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     // (row-major: key, 8-dim group) and of V (key-fastest, for the transpose)
     half8 kreg[PER], vreg[PER];
     auto fetch = [&](uint32_t k0) {
+        if (k0 + kFlashN <= a.kl) {   // a whole tile: no per-row bounds test
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const uint32_t e = tid + u * THREADS;
+                const uint32_t kk = k0 + e / (D / 8), kc = e % (D / 8);
+                const uint32_t vk = k0 + e % kFlashN, vc = e / kFlashN;
+                kreg[u] = *reinterpret_cast<const half8 *>(k + (kv_base + kk) * D + kc * 8);
+                vreg[u] = *reinterpret_cast<const half8 *>(v + (kv_base + vk) * D + vc * 8);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
             const uint32_t e = tid + u * THREADS;
@@ -422,7 +507,6 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
             // the wave, so no per-score bounds or causal test is needed
             const bool interior = k0 + kFlashN <= a.kl &&
                                   (!a.causal || (uint64_t)k0 + kFlashN - 1 <= (uint64_t)qw + a.causal_offset);
-            float local_max = neg_inf;
             // the two 32-key halves are independent accumulation chains:
             // interleaved, each MFMA's latency is covered by the other's
             float16v st[2];
@@ -430,6 +514,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
             for (int hblk = 0; hblk < 2; ++hblk)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) st[hblk][r] = 0.0f;
+            mfma_phase_begin();
 #pragma unroll
             for (int c = 0; c < KC; ++c)
 #pragma unroll
@@ -439,69 +524,105 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                     st[hblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], st[hblk], 0, 0, 0);
                 }
             lds_read_ahead<2 * KC>();
-            // scores are kept in log2 units: s * log2(e); the interior test is
-            // taken once per tile (inside the unrolled loop it became one
-            // branch per score)
+            mfma_phase_end();
+            // Scores are in log2 units: s = raw * scale2 (+ mask * log2 e).
+            // Without a mask (and with scale2 > 0) st keeps the raw products
+            // and sc = scale2 is applied inside exp2's fma; max_r(raw) * scale2
+            // == max_r(raw * scale2) since rounding is monotone. The kMask
+            // variant (also run for a scale <= 0, with or without a mask)
+            // turns st into s and uses sc = 1 (fma(s, 1, -m) == s - m). The
+            // interior test is taken once per tile (inside the unrolled loop
+            // it became one branch per score).
             auto score = [&](float raw, uint32_t kk, bool edge) {
                 float s = raw * scale2;
-                if constexpr (kMask) {
-                    if (kk < a.kl && q_live)
-                        s = __builtin_fmaf((float)mask[(size_t)qi * a.kl + kk], kLog2e, s);
-                }
+                if (mask != nullptr && kk < a.kl && q_live)
+                    s = __builtin_fmaf((float)mask[(size_t)qi * a.kl + kk], kLog2e, s);
                 if (edge && (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)))
                     s = neg_inf;
                 return s;
             };
-            // four independent max chains instead of one of 32
-            float part_max[4] = {neg_inf, neg_inf, neg_inf, neg_inf};
-            if (interior) {
-#pragma unroll
-                for (int hblk = 0; hblk < 2; ++hblk)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, false);
-                        part_max[r % 4] = fmaxf(part_max[r % 4], st[hblk][r]);
-                    }
-            } else {
-#pragma unroll
-                for (int hblk = 0; hblk < 2; ++hblk)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        st[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, true);
-                        part_max[r % 4] = fmaxf(part_max[r % 4], st[hblk][r]);
-                    }
-            }
-            local_max = fmaxf(fmaxf(part_max[0], part_max[1]), fmaxf(part_max[2], part_max[3]));
-            const float m_new = fmaxf(m, pair_max(local_max));
-            const bool none = m_new == neg_inf;   // nothing visible to this query yet
-            if (wave_any(none)) {
-                // a NaN score is dropped while nothing is visible; remember it
-                // (elsewhere it reaches the sum and makes the row NaN itself)
-                bool local_nan = false;
-#pragma unroll
-                for (int r = 0; r < 32; ++r) local_nan = local_nan || st[r / 16][r % 16] != st[r / 16][r % 16];
-                nan_seen = nan_seen || (none && local_nan);
-            }
-            const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+            // the online-softmax step for scores sv (s = sv * sc): P of the
+            // tile into pf, m, l and o updated
             half8 pf[4];
-            float part_sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            auto softmax = [&](const float16v (&sv)[2], float sc) {
+                // four independent max chains instead of one of 32
+                float part_max[4] = {neg_inf, neg_inf, neg_inf, neg_inf};
 #pragma unroll
-            for (int r = 0; r < 32; ++r) {
-                const float p = none ? 0.0f : __builtin_amdgcn_exp2f(st[r / 16][r % 16] - m_new);
-                part_sum[r % 4] += p;
-                pf[r / 8][r % 8] = (_Float16)p;
-            }
-            const float local_sum = (part_sum[0] + part_sum[1]) + (part_sum[2] + part_sum[3]);
-            l = l * alpha + pair_sum(local_sum);
-            m = m_new;
-            const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
-            if (rescale) {
+                for (int r = 0; r < 32; ++r) part_max[r % 4] = fmaxf(part_max[r % 4], sv[r / 16][r % 16]);
+                const float tile_max =
+                    pair_max(fmaxf(fmaxf(part_max[0], part_max[1]), fmaxf(part_max[2], part_max[3]))) * sc;
+                // Lazy rescale: the running max m (and with it o and l) moves
+                // only when some lane's maximum grows by more than
+                // 2^kLazyLog2; until then p = 2^(s - m) <= 2^kLazyLog2, well
+                // inside f16's range.
+                const float m_cand = fmaxf(m, tile_max);
+                if (__builtin_amdgcn_ballot_w64(m_cand > m + kLazyLog2) != 0) {
+                    const float alpha = m_cand == neg_inf ? 1.0f : __builtin_amdgcn_exp2f(m - m_cand);
+                    l *= alpha;
 #pragma unroll
-                for (int tt = 0; tt < VT; ++tt)
+                    for (int tt = 0; tt < VT; ++tt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
+                        for (int r = 0; r < 16; ++r) o[tt][r] *= alpha;
+                    m = m_cand;
+                }
+                const bool none = m == neg_inf;   // nothing visible to this query yet
+                if (wave_any(none)) {
+                    // a NaN score while nothing is visible is remembered: the
+                    // row is NaN if a key becomes visible later (its p, NaN,
+                    // also reaches o and l)
+                    bool local_nan = false;
+#pragma unroll
+                    for (int r = 0; r < 32; ++r) local_nan = local_nan || sv[r / 16][r % 16] != sv[r / 16][r % 16];
+                    nan_seen = nan_seen || (none && local_nan);
+                }
+                // with nothing visible every non-NaN score is -inf: p = 2^-inf = 0
+                const float m_use = none ? 0.0f : m;
+#pragma unroll
+                for (int r = 0; r < 32; ++r)
+                    pf[r / 8][r % 8] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[r / 16][r % 16], sc, -m_use));
+                // the row sum of P as the MFMA sees it (f16), by v_dot2 with {1, 1}
+                const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
+                float part_sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        part_sum[j] = __builtin_amdgcn_fdot2(half2_t{pf[c][2 * j], pf[c][2 * j + 1]}, ones,
+                                                             part_sum[j], false);
+                l += pair_sum((part_sum[0] + part_sum[1]) + (part_sum[2] + part_sum[3]));
+            };
+            if constexpr (kMask) {
+                float16v sv[2];
+                if (interior) {
+#pragma unroll
+                    for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            sv[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, false);
+                } else {
+#pragma unroll
+                    for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            sv[hblk][r] = score(st[hblk][r], k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4, true);
+                }
+                softmax(sv, 1.0f);
+            } else {
+                // raw products, scale2 > 0: keys out of range or past the
+                // causal limit become -inf in place
+                if (!interior) {
+#pragma unroll
+                    for (int hblk = 0; hblk < 2; ++hblk)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const uint32_t kk = k0 + 32 * hblk + 8 * (r / 4) + 4 * half + r % 4;
+                            if (kk >= a.kl || (a.causal && (uint64_t)kk > lane_last_key)) st[hblk][r] = neg_inf;
+                        }
+                }
+                softmax(st, scale2);
             }
             // the VT output tiles are independent chains: issue them side by side
+            mfma_phase_begin();
 #pragma unroll
             for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -511,6 +632,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
                     o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[tt], 0, 0, 0);
                 }
             lds_read_ahead<4 * VT>();
+            mfma_phase_end();
         }
         if (more) stash(buf ^ 1);
         __syncthreads();
@@ -518,8 +640,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
     if (!q_live) return;
     if constexpr (kSplit) {
-        write_partial<D, VT>(a, split, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
-        return;
+        if (item.parts > 1) {
+            write_partial<D, VT>(a, item.part, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
+            return;
+        }
     }
     const bool zero = !__builtin_isfinite(m);
     const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
@@ -575,12 +699,8 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
     const uint32_t col = lane & 31, half = lane >> 5;
-    const uint32_t qblocks = (a.ql + BM - 1) / BM;
-    const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-    const uint32_t split = kSplit ? logical % a.splits : 0;
-    const uint32_t pair = kSplit ? logical / a.splits : logical;
-    const uint32_t qblock = pair % qblocks;
-    const uint32_t bh = pair / qblocks;
+    const FlashItem item = flash_item(a, blockIdx.x);
+    const uint32_t qblock = item.qblock, bh = item.bh;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
     const uint32_t qw = qblock * BM + wave * 32;
@@ -612,12 +732,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     float m = neg_inf, l = 0.0f;
     bool nan_seen = false;
 
-    const uint32_t block_last_q = min(qblock * BM + BM - 1, a.ql - 1);
-    const uint64_t key_end = a.causal ? min((uint64_t)a.kl, (uint64_t)block_last_q + a.causal_offset + 1)
-                                      : (uint64_t)a.kl;
-    const uint32_t all_tiles = (uint32_t)((key_end + KN - 1) / KN);
-    const uint32_t share = kSplit ? (all_tiles + a.splits - 1) / a.splits : all_tiles;
-    const uint32_t t_begin = min(split * share, all_tiles);
+    const uint32_t all_tiles = flash_tiles(a.ql, a.kl, a.causal != 0, a.causal_offset, BM, KN,
+                                           qblock);
+    const uint32_t share = (all_tiles + item.parts - 1) / item.parts;
+    const uint32_t t_begin = min(item.part * share, all_tiles);
     const uint32_t tiles = min(t_begin + share, all_tiles);
     const bool wave_live = qw < a.ql;
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
@@ -738,8 +856,10 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
     if (!q_live) return;
     if constexpr (kSplit) {
-        write_partial<D, VT>(a, split, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
-        return;
+        if (item.parts > 1) {
+            write_partial<D, VT>(a, item.part, (size_t)bh * a.ql + qi, half, o, m, l, nan_seen);
+            return;
+        }
     }
     const bool zero = !__builtin_isfinite(m);
     const float inverse = l == 0.0f ? 0.0f : 1.0f / l;
@@ -801,50 +921,104 @@ hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out
 namespace {
 
 // Flash path choice for a shape: 128-query blocks (4 waves) when that gives
-// at least two blocks per CU, else 64-query blocks; a grid still short of
-// that splits each query block's key range over up to 8 blocks, merged by
-// sdpa_combine_kernel: toward 2 blocks per CU with >= 256 keys per split for
-// f16 (a 64-key tile is cheap, so a split must amortise its fixed cost), and
-// toward 4 blocks per CU with >= 128 keys for f32 (32-key tiles of 64
-// MFMAs each). Measured on the 12 x 1024 x 1024 x 64 shape.
+// at least two blocks per CU, else 64-query blocks. The work is then cut
+// into items and ordered longest first. With a workspace, query blocks whose
+// key range is long against the whole launch are split: target
+// split_tiles = max(total key tiles / slots, kMinPartTiles), slots being
+// the blocks resident at once (2 per CU for f16, 4 for f32, whose 32-key
+// tiles are cheaper). A causal launch of equal query blocks has ~2x
+// more tiles in its last block than on average, and without the split that
+// block's length is the launch's time. Items beyond kMaxFlashItems per
+// (batch, head): descending query blocks, no split.
 struct FlashPlan {
     bool flash = false;
     bool wide = false;
-    size_t grid = 0;       // blocks before splitting
-    uint32_t splits = 1;
+    uint32_t bm = 64, tk = 64;
+    uint32_t qblocks = 0, items = 0;
+    uint32_t split_tiles = 0;
+    uint32_t max_parts = 1;
+    uint32_t first_split = 0;   // first split query block
+    bool table = false, xcd_heads = false;
+    uint32_t item[kMaxFlashItems] = {};
 };
 
-FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32) {
+FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal, bool split) {
     FlashPlan p;
     const uint64_t lim = 0x7fffffffull;
     if (!aligned || sh.head_dim != sh.value_dim || (sh.head_dim != 64 && sh.head_dim != 128) ||
         !sh.batch || !sh.q_heads || !sh.kv_heads || sh.q_heads % sh.kv_heads != 0 ||
         !sh.q_len || sh.q_len > lim || !sh.kv_len || sh.kv_len > lim ||
-        sh.batch * sh.q_heads * ((sh.q_len + 63) / 64) > lim / 8)
+        sh.batch * sh.q_heads * ((sh.q_len + 63) / 64) > lim / (8 * kMaxKeyParts))
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
     p.wide = ((sh.q_len + 127) / 128) * bhs >= 512;
-    p.grid = ((sh.q_len + (p.wide ? 127 : 63)) / (p.wide ? 128 : 64)) * bhs;
-    if (!p.wide) {
-        const size_t target = f32 ? 1024 : 512;
-        size_t want = (target + p.grid - 1) / p.grid;
-        const size_t by_keys = sh.kv_len / (f32 ? 128 : 256);
-        want = want < by_keys ? want : by_keys;
-        p.splits = (uint32_t)(want < 1 ? 1 : want > 8 ? 8 : want);
+    p.bm = p.wide ? 128 : 64;
+    p.tk = f32 ? 32 : 64;
+    p.qblocks = (uint32_t)((sh.q_len + p.bm - 1) / p.bm);
+    p.items = p.qblocks;
+    p.first_split = p.qblocks;
+    p.xcd_heads = (sh.batch * sh.kv_heads) % 8 == 0;
+    if (p.qblocks > kMaxFlashItems) return p;
+    const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
+    const uint32_t offset = kl > ql ? kl - ql : 0;
+    auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
+    if (split) {
+        uint64_t total = 0;
+        for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
+        total *= bhs;
+        const uint64_t slots = f32 ? 1024 : 512;
+        const uint64_t target = (total + slots - 1) / slots;
+        p.split_tiles = (uint32_t)(target > kMinPartTiles ? target : kMinPartTiles);
     }
+    struct Item {
+        uint32_t size, qblock, part, parts;
+    };
+    Item list[kMaxFlashItems];
+    uint32_t n = 0;
+    for (uint32_t j = 0; j < p.qblocks; ++j) {
+        const uint32_t t = tiles(j), parts = split_parts(t, p.split_tiles);
+        const uint32_t share = (t + parts - 1) / parts;
+        if (n + parts > kMaxFlashItems) {   // too many: descending query blocks, whole
+            p.split_tiles = 0;
+            return p;
+        }
+        for (uint32_t q = 0; q < parts; ++q) {
+            const uint32_t lo = q * share < t ? q * share : t;
+            const uint32_t hi = lo + share < t ? lo + share : t;
+            list[n++] = Item{hi - lo, j, q, parts};
+        }
+        if (parts > p.max_parts) p.max_parts = parts;
+        if (parts > 1 && j < p.first_split) p.first_split = j;
+    }
+    std::stable_sort(list, list + n, [](const Item &x, const Item &y) {
+        return x.size != y.size ? x.size > y.size : x.qblock > y.qblock;
+    });
+    p.items = n;
+    p.table = true;
+    for (uint32_t r = 0; r < n; ++r)
+        p.item[r] = list[r].qblock | list[r].part << 16 | list[r].parts << 24;
+    if (p.max_parts == 1) p.split_tiles = 0;
     return p;
 }
 
-size_t partial_bytes(const k::SdpaShape &sh, uint32_t splits) {
+size_t partial_bytes(const k::SdpaShape &sh, uint32_t parts) {
     const size_t rows = sh.batch * sh.q_heads * sh.q_len;
-    return (size_t)splits * rows * (sh.head_dim + 4) * sizeof(float);
+    return (size_t)parts * rows * (sh.head_dim + 4) * sizeof(float);
 }
 
-// Arguments of the flash kernels; the split buffers are bound when the plan
-// splits and the caller's workspace holds them (otherwise no split).
+// The plan for a launch: split only when the caller's workspace holds the
+// partial results.
+FlashPlan launch_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal,
+                      size_t workspace_bytes, const void *workspace) {
+    const FlashPlan p = flash_plan(sh, aligned, f32, causal, true);
+    if (p.max_parts > 1 && (workspace == nullptr || workspace_bytes < partial_bytes(sh, p.max_parts)))
+        return flash_plan(sh, aligned, f32, causal, false);
+    return p;
+}
+
 SdpaArgs flash_args(const FlashPlan &p, const k::SdpaShape &sh, float scale, bool causal,
-                    void *workspace, size_t workspace_bytes) {
+                    void *workspace) {
     SdpaArgs a{};
     a.batch = (uint32_t)sh.batch;
     a.qh = (uint32_t)sh.q_heads;
@@ -856,33 +1030,39 @@ SdpaArgs flash_args(const FlashPlan &p, const k::SdpaShape &sh, float scale, boo
     a.causal_offset = a.kl > a.ql ? a.kl - a.ql : 0;
     a.scale = scale;
     a.causal = causal ? 1 : 0;
-    a.splits = 1;
-    if (p.splits > 1 && workspace != nullptr &&
-        workspace_bytes >= partial_bytes(sh, p.splits)) {
+    a.items = p.items;
+    a.qblocks = p.qblocks;
+    a.split_tiles = p.split_tiles;
+    a.table = p.table ? 1 : 0;
+    a.xcd_heads = p.xcd_heads ? 1 : 0;
+    for (uint32_t r = 0; r < p.items && p.table; ++r) a.item[r] = p.item[r];
+    if (p.max_parts > 1) {
         const size_t rows = sh.batch * sh.q_heads * sh.q_len;
-        a.splits = p.splits;
         a.part_o = static_cast<float *>(workspace);
-        a.part_ml = reinterpret_cast<f32x4 *>(a.part_o + (size_t)p.splits * rows * sh.head_dim);
+        a.part_ml = reinterpret_cast<f32x4 *>(a.part_o + (size_t)p.max_parts * rows * sh.head_dim);
     }
     return a;
 }
 
 template <typename S>
-hipError_t combine_splits(const SdpaArgs &a, S *out, hipStream_t s) {
-    const size_t n = (size_t)a.batch * a.qh * a.ql * (a.dim / 4);
+hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStream_t s) {
+    const uint32_t first_row = p.first_split * p.bm;
+    const size_t n = (size_t)a.batch * a.qh * (a.ql - first_row) * (a.dim / 4);
     hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2>),
-                       dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, a, out);
+                       dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, a, out,
+                       p.bm, p.tk, first_row);
     return hipGetLastError();
 }
 
 }  // namespace
 
-// One flash launch for the plan's (D, BM) with the mask / split variant.
+// One flash launch for the plan's (D, BM) with the general (mask) / split
+// variant.
 #define ICSDK_FLASH_VARIANTS(KERNEL, D, BM, Q, K, V, M, O)                                         \
     do {                                                                                           \
-        if ((M) != nullptr && split)                                                               \
+        if (general && split)                                                                      \
             hipLaunchKernelGGL((KERNEL<D, BM, true, true>), grid, block, 0, s, Q, K, V, M, O, a);  \
-        else if ((M) != nullptr)                                                                   \
+        else if (general)                                                                          \
             hipLaunchKernelGGL((KERNEL<D, BM, true, false>), grid, block, 0, s, Q, K, V, M, O, a); \
         else if (split)                                                                            \
             hipLaunchKernelGGL((KERNEL<D, BM, false, true>), grid, block, 0, s, Q, K, V, M, O, a); \
@@ -902,23 +1082,24 @@ hipError_t combine_splits(const SdpaArgs &a, S *out, hipStream_t s) {
 
 namespace k {
 
-size_t sdpa_workspace_bytes(const SdpaShape &shape, bool f32) {
-    const FlashPlan p = flash_plan(shape, true, f32);
-    return p.flash && p.splits > 1 ? partial_bytes(shape, p.splits) : 0;
+size_t sdpa_workspace_bytes(const SdpaShape &shape, bool f32, bool causal) {
+    const FlashPlan p = flash_plan(shape, true, f32, causal, true);
+    return p.flash && p.max_parts > 1 ? partial_bytes(shape, p.max_parts) : 0;
 }
 
 hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
                     float *out, const SdpaShape &shape, float scale, bool causal,
                     void *workspace, size_t workspace_bytes, hipStream_t s) {
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const FlashPlan plan = flash_plan(shape, aligned, true);
+    const FlashPlan plan = launch_plan(shape, aligned, true, causal, workspace_bytes, workspace);
     if (!plan.flash) return launch_sdpa<float>(q, k, v, mask, out, shape, scale, causal, s);
-    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
-    const bool split = a.splits > 1;
-    const dim3 grid((unsigned)(plan.grid * a.splits)), block(plan.wide ? 256 : 128);
+    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace);
+    const bool split = plan.max_parts > 1;
+    const bool general = mask != nullptr;
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(plan.wide ? 256 : 128);
     ICSDK_FLASH_SHAPES(sdpa_flash_f32_kernel, q, k, v, mask, out);
     const hipError_t status = hipGetLastError();
-    return status != hipSuccess || !split ? status : combine_splits(a, out, s);
+    return status != hipSuccess || !split ? status : combine_splits(a, plan, out, s);
 }
 
 hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
@@ -927,15 +1108,18 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     auto h = [](const uint16_t *p) { return reinterpret_cast<const _Float16 *>(p); };
     _Float16 *o16 = reinterpret_cast<_Float16 *>(out);
     const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) == 0;
-    const FlashPlan plan = flash_plan(shape, aligned, false);
+    const FlashPlan plan = launch_plan(shape, aligned, false, causal, workspace_bytes, workspace);
     if (!plan.flash)
         return launch_sdpa<_Float16>(h(q), h(k), h(v), h(mask), o16, shape, scale, causal, s);
-    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace, workspace_bytes);
-    const bool split = a.splits > 1;
-    const dim3 grid((unsigned)(plan.grid * a.splits)), block(plan.wide ? 256 : 128);
+    const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace);
+    const bool split = plan.max_parts > 1;
+    // the raw-product softmax needs scale > 0; other scales take the general
+    // (mask) variant, whose mask may be null
+    const bool general = mask != nullptr || !(scale > 0.0f);
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(plan.wide ? 256 : 128);
     ICSDK_FLASH_SHAPES(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
     const hipError_t status = hipGetLastError();
-    return status != hipSuccess || !split ? status : combine_splits(a, o16, s);
+    return status != hipSuccess || !split ? status : combine_splits(a, plan, o16, s);
 }
 
 }  // namespace k

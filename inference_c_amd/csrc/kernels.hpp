@@ -112,10 +112,10 @@ hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t
 struct SdpaShape {
     size_t batch, q_heads, kv_heads, q_len, kv_len, head_dim, value_dim;
 };
-// `workspace` (may be null) lets a small grid split each query block's key
-// range over several blocks: sdpa_workspace_bytes(shape, f32) bytes, 0 when
-// the shape would not split.
-size_t sdpa_workspace_bytes(const SdpaShape &shape, bool f32);
+// `workspace` (may be null) lets the flash path split the key range of long
+// query blocks over several blocks: sdpa_workspace_bytes(shape, f32, causal)
+// bytes, 0 when the shape would not split.
+size_t sdpa_workspace_bytes(const SdpaShape &shape, bool f32, bool causal);
 hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float *mask,
                     float *out, const SdpaShape &shape, float scale, bool causal,
                     void *workspace, size_t workspace_bytes, hipStream_t s);
