@@ -344,15 +344,15 @@ __device__ inline void write_partial(const SdpaArgs &a, uint32_t split, size_t r
 // block never sees fewer keys): M = max of the parts' maxima; a row whose M
 // is not finite is zero; a NaN flag with a finite M makes the row NaN;
 // otherwise out = (sum_s w_s o_s) * (1 / sum_s w_s l_s) with w_s =
-// exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per 4
-// output elements.
+// exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per 8
+// output elements (dim % 8 == 0 on the flash path).
 template <typename S, bool kLog2>
 __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__restrict__ out,
                                                               uint32_t bm, uint32_t tk,
                                                               uint32_t first_row) {
     const size_t rows = (size_t)a.batch * a.qh * a.ql;
     const uint32_t suffix = a.ql - first_row;
-    const uint32_t groups = a.dim / 4;
+    const uint32_t groups = a.dim / 8;
     const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
     if (i >= (size_t)a.batch * a.qh * suffix * groups) return;
     const size_t srow = i / groups;
@@ -368,28 +368,36 @@ __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__r
         big = fmaxf(big, ml.x);
         nan_flag = nan_flag || ml.z != 0.0f;
     }
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
     float total = 0.0f;
     if (__builtin_isfinite(big)) {
         for (uint32_t s = 0; s < splits; ++s) {
             const f32x4 ml = a.part_ml[(size_t)s * rows + row];
-            // a split that saw no visible key has sum 0 and output 0; every
-            // other split is added even at weight 0, so a NaN it holds stays
+            // a part that saw no visible key has sum 0 and output 0; every
+            // other part is added even at weight 0, so a NaN it holds stays
             const float w = ml.x == -__builtin_inff() ? 0.0f
                             : kLog2 ? __builtin_amdgcn_exp2f(ml.x - big) : expf(ml.x - big);
-            const f32x4 po = *reinterpret_cast<const f32x4 *>(
-                a.part_o + ((size_t)s * rows + row) * a.dim + 4 * g);
+            const f32x4 *po = reinterpret_cast<const f32x4 *>(
+                a.part_o + ((size_t)s * rows + row) * a.dim + 8 * g);
             total += w * ml.y;
-            acc += w * po;
+            lo += w * po[0];
+            hi += w * po[1];
         }
     }
     const bool zero = !__builtin_isfinite(big);
     const float inverse = total == 0.0f ? 0.0f : 1.0f / total;
     const float nan = __builtin_nanf("");
-    S *orow = out + row * a.dim + 4 * g;
+    S res[8] __attribute__((aligned(16)));
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        orow[j] = (S)(zero ? 0.0f : nan_flag ? nan : acc[j] * inverse);
+    for (int j = 0; j < 8; ++j)
+        res[j] = (S)(zero ? 0.0f : nan_flag ? nan : (j < 4 ? lo[j] : hi[j - 4]) * inverse);
+    S *orow = out + row * a.dim + 8 * g;
+    if constexpr (sizeof(S) == 2) {
+        *reinterpret_cast<u32x4 *>(orow) = *reinterpret_cast<const u32x4 *>(res);
+    } else {
+        reinterpret_cast<u32x4 *>(orow)[0] = reinterpret_cast<const u32x4 *>(res)[0];
+        reinterpret_cast<u32x4 *>(orow)[1] = reinterpret_cast<const u32x4 *>(res)[1];
+    }
 }
 
 template <int D, int BM, bool kMask, bool kSplit>
@@ -1047,7 +1055,7 @@ SdpaArgs flash_args(const FlashPlan &p, const k::SdpaShape &sh, float scale, boo
 template <typename S>
 hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStream_t s) {
     const uint32_t first_row = p.first_split * p.bm;
-    const size_t n = (size_t)a.batch * a.qh * (a.ql - first_row) * (a.dim / 4);
+    const size_t n = (size_t)a.batch * a.qh * (a.ql - first_row) * (a.dim / 8);
     hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2>),
                        dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, a, out,
                        p.bm, p.tk, first_row);

@@ -85,6 +85,54 @@ def test_device_sdpa(sdk, orc, shape, dtype, causal, masked):
     check(got, want, weight, dtype, f"{shape} causal={causal} mask={masked}")
 
 
+# MFMA-path shapes with several 64-key tiles per row
+RAMP_SHAPES = [(1, 2, 1, 64, 2048, 128, 128), (1, 4, 4, 256, 256, 64, 64)]
+
+
+@pytest.mark.parametrize("shape", RAMP_SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("direction", [1.0, -1.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_growing_row_maxima(sdk, orc, shape, dtype, direction, causal):
+    """Scores that climb (or fall) steadily along the keys, 60 log2 units
+    over the row for f16: the running maximum of the f16 kernel moves on
+    some tiles (growth past 2^8 since it last moved) and stays on others
+    (probabilities up to 2^8 in the f16 P operand); falling scores keep the
+    first tile's maximum throughout. f32 climbs 20 log2 units: one rounding
+    of a score s moves exp(s) by |s| ulps, which at 40 nats exceeds the f32
+    bound whatever the kernel."""
+    b, h, kh, lq, lk, d, dv = shape
+    q, k, v, _ = inputs(orc, shape, dtype, 31, False)
+    scale = 1.0 / np.sqrt(d)
+    climb = 60.0 if dtype == "f16" else 20.0   # log2 units from the first key to the last
+    reach = climb / (4.0 * scale * np.log2(np.e))   # q[..., 0] * k[..., -1, 0] * scale
+    q[..., 0] = 4.0
+    k[..., :, 0] = (direction * reach * np.arange(lk) / lk).astype(k.dtype)
+    got = run_device(sdk, q, k, v, None, scale, causal, dtype)
+    want = orc.sdpa(q, k, v, None, scale, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
+    check(got, want, weight, dtype, f"{shape} direction={direction} causal={causal}")
+
+
+@pytest.mark.parametrize("dtype,scale", [("f16", -0.2), ("f16", 0.0), ("f16", 3.0),
+                                         ("f32", -0.2), ("f32", 0.0), ("f32", 0.2)])
+@pytest.mark.parametrize("shape", [(1, 4, 1, 300, 300, 128, 128), (1, 2, 1, 40, 2048, 128, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_scales(sdk, orc, scale, shape, dtype, causal):
+    """Scales other than 1/sqrt(d) on the MFMA path, unsplit and split: a
+    negative or zero scale takes the f16 kernel's general variant (raw
+    products cannot carry the scale into the maximum), a large one makes
+    the softmax nearly one-hot. f32 stops at 0.2: its scores' own rounding
+    (|q.k| up to ~40 for d = 128, summed in another order than the
+    oracle's, ~3e-5 apart) times the scale is the relative error of p, and
+    past ~0.3 that alone exceeds the f32 bound."""
+    q, k, v, _ = inputs(orc, shape, dtype, 32, False)
+    got = run_device(sdk, q, k, v, None, scale, causal, dtype)
+    want = orc.sdpa(q, k, v, None, scale, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
+    check(got, want, weight, dtype, f"{shape} scale={scale} causal={causal}")
+
+
 def table_slots(sdk):
     sdk.lib.tensor_attention_cuda_backend.restype = ctypes.c_void_p
     return ctypes.cast(sdk.lib.tensor_attention_cuda_backend(), ctypes.POINTER(ctypes.c_void_p))
