@@ -295,9 +295,10 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
             lambda s: sdk.call("tensor_embedding_lookup_f16", emb_table, s[0], s[1]),
             2 * tokens * width * 2 + tokens * 4, tokens * width)
     del emb_table
-    # quantized linear (decode GEMV, HBM-bound on the packed weights): a
-    # [28672, 8192] Q8_0 / Q4_0 matrix (a 70B-class MLP up+gate projection)
-    # times 1 or 4 f16 rows; synthetic packed bytes with an f16 scale of 2^-7
+    # quantized linear (HBM-bound on the packed weights): a [28672, 8192]
+    # Q8_0 / Q4_0 matrix (a 70B-class MLP up+gate projection) times 1 or 4 f16
+    # rows (the GEMV) or 16 rows (the MFMA kernel: small-batch decode);
+    # synthetic packed bytes with an f16 scale of 2^-7
     rng = np.random.default_rng(7)
     def packed_weights(out, inw, block):
         raw = rng.integers(0, 256, size=(out, inw // 32, block), dtype=np.uint8)
@@ -306,7 +307,7 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     for fmt, block in (("q8_0", 34), ("q4_0", 18)):
         out_f, in_f = 28672, 8192
         host_w = packed_weights(out_f, in_f, block)
-        for rows in ((1, 4) if fmt == "q8_0" else (1,)):
+        for rows in ((1, 4, 16) if fmt == "q8_0" else (1,)):
             def quant_set(rows=rows, host_w=host_w):
                 return (T("u8", host_w.shape).upload(host_w),
                         filled("f16", (rows, in_f), "normal", 7, 3, 0.0, 1.0),

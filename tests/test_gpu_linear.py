@@ -296,6 +296,7 @@ def test_quantize_known_bytes(sdk):
 QUANT_SHAPES = [  # rows, in, out
     (1, 32, 1), (1, 64, 7), (1, 2048, 256), (2, 4096, 130), (3, 96, 33), (4, 1024, 64),
     (5, 512, 40), (8, 256, 16), (17, 2080, 24), (64, 768, 96), (1, 8192, 512),
+    (6, 8192, 100), (33, 544, 50),   # MFMA path: ragged outputs; a partial 32-row group, short key quarters
 ]
 
 
