@@ -252,7 +252,7 @@ int host_embedding(const T *table, const uint32_t *ids, T *out, size_t rows, siz
     void *po = st.out(out, n * sizeof(T));
     if (st.failed()) return 0;
     return st.finish(k::embedding_gather(TENSOR_DTYPE_U32, device_table, table_rows,
-                                         width * sizeof(T), sizeof(T), pi, rows, po,
+                                         width * sizeof(T), sizeof(T), pi, rows, po, nullptr,
                                          st.stream()))
                ? 1
                : 0;

@@ -5,11 +5,12 @@
 // element type.
 //
 // check  - one 1024-lane block scans the ids (16-byte vectors, several in
-//          flight per lane) and writes 1 to `flag` when any is negative or
-//          at/past the table's row count, else 0 (the public entry points
-//          reject such calls before any row is written; one block needs no
-//          atomics and no pre-cleared flag, and `flag` may be pinned host
-//          memory, read after one stream wait);
+//          flight per lane) and writes 1 to `flag` (pinned host memory)
+//          and to `skip` (device memory) when any is negative or at/past
+//          the table's row count, else 0; one block needs no atomics and no
+//          pre-cleared words. The public entry points enqueue the gather
+//          right behind it with `skip`, so a rejected call writes no row,
+//          and wait only for the check before reading `flag`;
 // gather - rows that are whole 16-byte vectors (and aligned): one output
 //          vector per lane on a one-shot grid; the lane's row and column
 //          come from a multiply-high division, its id from the (cached) id
@@ -39,12 +40,13 @@ constexpr int kCheckUnroll = 4;  // 16-byte vectors in flight per lane
 
 // One block scans all ids: each lane keeps kCheckUnroll 16-byte vectors of
 // ids in flight per step (a 1024-lane block covers 64 KiB per step), then a
-// scalar tail; the verdict is written by lane 0 to `flag`, which may be a
-// word of pinned host memory.
+// scalar tail; the verdict is written by lane 0 to `flag` (a word of pinned
+// host memory) and to the device word `skip`.
 template <typename I>
 __global__ __launch_bounds__(kCheckBlock) void embedding_check_kernel(const I *__restrict__ ids,
                                                                       size_t count, uint64_t rows,
-                                                                      uint32_t *__restrict__ flag) {
+                                                                      uint32_t *__restrict__ flag,
+                                                                      uint32_t *__restrict__ skip) {
     constexpr int kPer = 16 / sizeof(I);
     // vector part only for a 16-byte aligned id buffer; otherwise all scalar
     const size_t nvec = ((uintptr_t)ids & 15u) ? 0 : count / kPer;
@@ -72,9 +74,12 @@ __global__ __launch_bounds__(kCheckBlock) void embedding_check_kernel(const I *_
         bad |= !index_ok(ids[i], rows, &id);
     }
     bad = __syncthreads_or(bad);
-    // system scope: visible to the host once the stream has been waited on
-    if (threadIdx.x == 0)
+    // system scope: visible to the host once it has waited for this kernel;
+    // the device word is read by the gather that follows on the stream
+    if (threadIdx.x == 0) {
         __hip_atomic_store(flag, bad ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        *skip = bad ? 1u : 0u;
+    }
 }
 
 template <typename I, bool kThrough>
@@ -82,7 +87,9 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_kernel(const u32x4 *_
                                                                   const I *__restrict__ ids,
                                                                   uint32_t *__restrict__ out,
                                                                   uint32_t nvec, FastDiv vpr,
-                                                                  uint64_t rows) {
+                                                                  uint64_t rows,
+                                                                  const uint32_t *__restrict__ skip) {
+    if (skip != nullptr && *skip != 0) return;   // the check rejected the call
     const uint32_t first = blockIdx.x * kBlock;
     const uint32_t v = first + threadIdx.x;
     if (v >= nvec) return;
@@ -98,7 +105,8 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_kernel(const u32x4 *_
 template <typename I, typename E>
 __global__ __launch_bounds__(kBlock) void embedding_gather_scalar_kernel(
     const E *__restrict__ table, const I *__restrict__ ids, E *__restrict__ out, size_t n,
-    size_t width, uint64_t rows) {
+    size_t width, uint64_t rows, const uint32_t *__restrict__ skip) {
+    if (skip != nullptr && *skip != 0) return;   // the check rejected the call
     const size_t stride = (size_t)gridDim.x * kBlock;
     for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         const size_t row = i / width, col = i - row * width;
@@ -110,15 +118,16 @@ __global__ __launch_bounds__(kBlock) void embedding_gather_scalar_kernel(
 
 template <typename I>
 hipError_t launch_check(const void *ids, size_t count, uint64_t rows, uint32_t *flag,
-                        hipStream_t s) {
+                        uint32_t *skip, hipStream_t s) {
     hipLaunchKernelGGL((embedding_check_kernel<I>), dim3(1), dim3(kCheckBlock), 0, s,
-                       static_cast<const I *>(ids), count, rows, flag);
+                       static_cast<const I *>(ids), count, rows, flag, skip);
     return hipGetLastError();
 }
 
 template <typename I>
 hipError_t launch_gather(const void *table, uint64_t rows, size_t row_bytes, size_t elem_bytes,
-                         const void *ids, size_t count, void *out, hipStream_t s) {
+                         const void *ids, size_t count, void *out, const uint32_t *skip,
+                         hipStream_t s) {
     const size_t out_bytes = count * row_bytes;
     const bool aligned = (((uintptr_t)table | (uintptr_t)out) & 15u) == 0;
     if (row_bytes % 16 == 0 && aligned && out_bytes / 16 < (size_t{1} << 32)) {
@@ -128,11 +137,11 @@ hipError_t launch_gather(const void *table, uint64_t rows, size_t row_bytes, siz
         if (write_through_for(out_bytes))
             hipLaunchKernelGGL((embedding_gather_kernel<I, true>), grid, block, 0, s,
                                static_cast<const u32x4 *>(table), static_cast<const I *>(ids),
-                               static_cast<uint32_t *>(out), nvec, vpr, rows);
+                               static_cast<uint32_t *>(out), nvec, vpr, rows, skip);
         else
             hipLaunchKernelGGL((embedding_gather_kernel<I, false>), grid, block, 0, s,
                                static_cast<const u32x4 *>(table), static_cast<const I *>(ids),
-                               static_cast<uint32_t *>(out), nvec, vpr, rows);
+                               static_cast<uint32_t *>(out), nvec, vpr, rows, skip);
         return hipGetLastError();
     }
     const size_t width = row_bytes / elem_bytes, n = count * width;
@@ -142,12 +151,12 @@ hipError_t launch_gather(const void *table, uint64_t rows, size_t row_bytes, siz
         hipLaunchKernelGGL((embedding_gather_scalar_kernel<I, uint32_t>), dim3((unsigned)grid),
                            dim3(kBlock), 0, s, static_cast<const uint32_t *>(table),
                            static_cast<const I *>(ids), static_cast<uint32_t *>(out), n, width,
-                           rows);
+                           rows, skip);
     else if (elem_bytes == 2)
         hipLaunchKernelGGL((embedding_gather_scalar_kernel<I, uint16_t>), dim3((unsigned)grid),
                            dim3(kBlock), 0, s, static_cast<const uint16_t *>(table),
                            static_cast<const I *>(ids), static_cast<uint16_t *>(out), n, width,
-                           rows);
+                           rows, skip);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -176,18 +185,18 @@ bool embedding_index_type(TensorDType dtype) {
 }
 
 hipError_t embedding_check(TensorDType index_dtype, const void *ids, size_t count,
-                           uint64_t table_rows, uint32_t *flag, hipStream_t s) {
-#define ICSDK_CHECK(I) launch_check<I>(ids, count, table_rows, flag, s)
+                           uint64_t table_rows, uint32_t *flag, uint32_t *skip, hipStream_t s) {
+#define ICSDK_CHECK(I) launch_check<I>(ids, count, table_rows, flag, skip, s)
     ICSDK_WITH_INDEX_TYPE(index_dtype, ICSDK_CHECK)
 #undef ICSDK_CHECK
 }
 
 hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t table_rows,
                             size_t row_bytes, size_t elem_bytes, const void *ids, size_t count,
-                            void *out, hipStream_t s) {
+                            void *out, const uint32_t *skip, hipStream_t s) {
     if (count == 0 || row_bytes == 0) return hipSuccess;
 #define ICSDK_GATHER(I) \
-    launch_gather<I>(table, table_rows, row_bytes, elem_bytes, ids, count, out, s)
+    launch_gather<I>(table, table_rows, row_bytes, elem_bytes, ids, count, out, skip, s)
     ICSDK_WITH_INDEX_TYPE(index_dtype, ICSDK_GATHER)
 #undef ICSDK_GATHER
 }

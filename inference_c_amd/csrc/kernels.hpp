@@ -98,13 +98,15 @@ hipError_t view_add_mul_f16(const uint16_t *x, const ViewArgs &v, const uint16_t
 // Embedding lookup: out[i, :] = table[ids[i], :] (rows of row_bytes bytes,
 // elements of elem_bytes = 2 or 4). ids are I16/U16/I32/U32/I64/U64; an id
 // that is negative or >= table_rows gives a zero row. embedding_check writes
-// 1 to the device word `flag` when any id is such, else 0 (one block).
+// 1 to `flag` (pinned host memory) and to the device word `skip` when any id
+// is such, else 0 (one block); embedding_gather writes nothing when `skip`
+// (may be null) holds a non-zero word.
 bool embedding_index_type(TensorDType dtype);
 hipError_t embedding_check(TensorDType index_dtype, const void *ids, size_t count,
-                           uint64_t table_rows, uint32_t *flag, hipStream_t s);
+                           uint64_t table_rows, uint32_t *flag, uint32_t *skip, hipStream_t s);
 hipError_t embedding_gather(TensorDType index_dtype, const void *table, uint64_t table_rows,
                             size_t row_bytes, size_t elem_bytes, const void *ids, size_t count,
-                            void *out, hipStream_t s);
+                            void *out, const uint32_t *skip, hipStream_t s);
 
 // Scaled dot-product attention with the accelerator semantics of the
 // reference (q [B,Hq,Lq,D], k [B,Hkv,Lkv,D], v [B,Hkv,Lkv,Dv], mask [Lq,Lkv]

@@ -485,6 +485,19 @@ bool host_index(Buf indices, size_t i, uint64_t *id) {
     }
 }
 
+// An event of the calling host thread for waiting on one point of the SDK
+// stream: created on first use and kept for the thread's lifetime (null if
+// it cannot be created; callers then wait for the whole stream).
+hipEvent_t thread_event() {
+    thread_local hipEvent_t event = nullptr;
+    thread_local bool tried = false;
+    if (!tried) {
+        tried = true;
+        if (hipEventCreateWithFlags(&event, hipEventDisableTiming) != hipSuccess) event = nullptr;
+    }
+    return event;
+}
+
 int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *out, char *error,
                      size_t capacity) {
     const bool f32 = dtype == TENSOR_DTYPE_F32;
@@ -516,7 +529,9 @@ int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *ou
         return 0;
     }
     // every index is checked before any row is written: on the host for host
-    // buffers, by a one-block kernel (and one wait) for device buffers
+    // buffers; for device buffers by a one-block kernel that also writes a
+    // device word the gather (enqueued right behind it) reads, so a rejected
+    // call writes no row, and the host waits for the check alone
     if (host) {
         for (size_t i = 0; i < count; ++i) {
             uint64_t id;
@@ -528,30 +543,42 @@ int embedding_lookup(TensorDType dtype, Buf table, Buf indices, TensorBuffer *ou
     }
     Staging st("embedding lookup", host, error, capacity);
     if (!st.begin()) return 0;
+    HostWord verdict;
+    ScratchBlock skip(host ? 0 : sizeof(uint32_t));
+    hipEvent_t checked = nullptr;
     if (!host) {
-        HostWord verdict;
-        if (verdict.get() == nullptr) {
-            set_error(error, capacity, "embedding lookup: cannot allocate pinned host memory");
+        if (verdict.get() == nullptr || skip.get() == nullptr) {
+            set_error(error, capacity, "embedding lookup: cannot allocate the index verdict");
             return 0;
         }
         if (!hip_ok(k::embedding_check(index_dtype, tensor_buffer_device_handle_internal(indices),
-                                       count, ts[0], verdict.get(), st.stream()),
-                    "embedding lookup: index check launch", error, capacity) ||
-            !hip_ok(hipStreamSynchronize(st.stream()), "embedding lookup: hipStreamSynchronize",
-                    error, capacity))
+                                       count, ts[0], verdict.get(),
+                                       static_cast<uint32_t *>(skip.get()), st.stream()),
+                    "embedding lookup: index check launch", error, capacity))
             return 0;
-        if (verdict.read() != 0) {
-            set_error(error, capacity, "%s", bad_index);
-            return 0;
-        }
+        checked = thread_event();
+        if (checked != nullptr && hipEventRecord(checked, st.stream()) != hipSuccess)
+            checked = nullptr;
     }
     const void *pt = src(st, table);
     const void *pi = src(st, indices);
     void *po = dst(st, out);
     if (st.failed()) return 0;
     const size_t elem = f32 ? 4 : 2;
-    const hipError_t status = k::embedding_gather(index_dtype, pt, ts[0], (size_t)ts[1] * elem,
-                                                  elem, pi, count, po, st.stream());
+    const hipError_t status =
+        k::embedding_gather(index_dtype, pt, ts[0], (size_t)ts[1] * elem, elem, pi, count, po,
+                            static_cast<const uint32_t *>(skip.get()), st.stream());
+    if (!host) {
+        // without the event, wait for the gather as well
+        if (!hip_ok(checked != nullptr ? hipEventSynchronize(checked)
+                                       : hipStreamSynchronize(st.stream()),
+                    "embedding lookup: waiting for the index check", error, capacity))
+            return 0;
+        if (verdict.read() != 0) {
+            set_error(error, capacity, "%s", bad_index);
+            return 0;
+        }
+    }
     return st.finish(status) ? 1 : 0;
 }
 

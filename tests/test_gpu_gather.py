@@ -84,15 +84,18 @@ def test_rejected_lookup_leaves_output(sdk, orc, device, bad):
 def test_device_index_check_positions(sdk, orc, index_type, count, position):
     """The device check scans 16-byte vectors of ids, several per lane per
     step, then a scalar tail: a bad id anywhere is found, a good batch
-    passes."""
+    passes. The gather is enqueued behind the check and skips every row on
+    a rejected call: the previous output stays."""
     rows, width = 1000, 8
     table = sdk.from_numpy(orc.normal((rows, width), 45, 0, 0.0, 1.0, "f16"))
     ids = ids_for(orc, count, rows, 45).astype(index_type)
     out = sdk.tensor("f16", (count, width))
     assert sdk.try_call("tensor_embedding_lookup_f16", table, sdk.from_numpy(ids), out)[0] == 1
+    good = out.download()
     ids[position] = rows if not np.issubdtype(index_type, np.signedinteger) or position % 2 else -1
     ok, msg = sdk.try_call("tensor_embedding_lookup_f16", table, sdk.from_numpy(ids), out)
     assert not ok and msg == "embedding index is negative or outside the table"
+    assert_bits_equal(out.download(), good, "output after a rejected call")
 
 
 def test_lookup_mixed_storage_rejected(sdk, orc):
