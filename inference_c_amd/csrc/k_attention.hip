@@ -932,12 +932,13 @@ namespace {
 // at least two blocks per CU, else 64-query blocks. The work is then cut
 // into items and ordered longest first. With a workspace, query blocks whose
 // key range is long against the whole launch are split: target
-// split_tiles = max(total key tiles / slots, kMinPartTiles), slots being
-// the blocks resident at once (2 per CU for f16, 4 for f32, whose 32-key
-// tiles are cheaper). A causal launch of equal query blocks has ~2x
-// more tiles in its last block than on average, and without the split that
-// block's length is the launch's time. Items beyond kMaxFlashItems per
-// (batch, head): descending query blocks, no split.
+// split_tiles = max(total key tiles / slots, kMinPartTiles). Measured over
+// slot targets 128 .. 3072: f16 256 (a split rarely pays for its merge:
+// causal 32 x 2048^2 D 128 66.5 us unsplit vs 69.2 in 2 parts, 12 x 1024^2
+// D 64 22.2 vs 23.0 in 3; tiny grids still split), f32 2048 (its 32-key
+// tiles of 64 MFMAs keep a block busy: 12 x 1024^2 D 64 103 us unsplit,
+// 56.3 in 6 parts, 55.3 in 8). Items beyond kMaxFlashItems per (batch,
+// head): descending query blocks, no split.
 struct FlashPlan {
     bool flash = false;
     bool wide = false;
@@ -975,7 +976,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
-        const uint64_t slots = f32 ? 1024 : 512;
+        const uint64_t slots = f32 ? 2048 : 256;
         const uint64_t target = (total + slots - 1) / slots;
         p.split_tiles = (uint32_t)(target > kMinPartTiles ? target : kMinPartTiles);
     }

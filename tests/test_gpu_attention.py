@@ -33,6 +33,7 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (3, 2, 2, 1, 77, 128, 128),     # MFMA path: one query
     (1, 2, 1, 40, 2048, 128, 128),  # MFMA path, key range split over 8 blocks
     (2, 3, 3, 100, 1500, 64, 64),   # MFMA path, key range split in 6 (f16) / 8 (f32, uneven) parts
+    (1, 2, 2, 600, 600, 64, 64),    # MFMA path, causal: long query blocks split, short ones whole
 ]
 
 
