@@ -928,17 +928,20 @@ hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out
 
 namespace {
 
-// Flash path choice for a shape: 128-query blocks (4 waves) when that gives
-// at least two blocks per CU, else 64-query blocks. The work is then cut
-// into items and ordered longest first. With a workspace, query blocks whose
-// key range is long against the whole launch are split: target
-// split_tiles = max(total key tiles / slots, kMinPartTiles). Measured over
-// slot targets 128 .. 3072: f16 256 (a split rarely pays for its merge:
-// causal 32 x 2048^2 D 128 66.5 us unsplit vs 69.2 in 2 parts, 12 x 1024^2
-// D 64 22.2 vs 23.0 in 3; tiny grids still split), f32 2048 (its 32-key
-// tiles of 64 MFMAs keep a block busy: 12 x 1024^2 D 64 103 us unsplit,
-// 56.3 in 6 parts, 55.3 in 8). Items beyond kMaxFlashItems per (batch,
-// head): descending query blocks, no split.
+// Flash path choice for a shape: 128-query blocks (4 waves sharing each K/V
+// tile) when there are at least 64 of them, else 64-query blocks (measured:
+// 12 x 1024^2 D 64 f16 20.1 us wide vs 22.2 narrow, 4 x 16 x 512^2 D 128
+// 21.1 vs 25.6, 32 x 1024^2 causal 33.2 vs 39.0, f32 4 x 16 x 512^2 56.6
+// vs 70.6). The work is then cut into items and ordered longest first.
+// With a workspace, query blocks whose key range is long against the whole
+// launch are split: target split_tiles = max(total key tiles / slots,
+// kMinPartTiles), slots measured over 128 .. 3072: f16 128 (a split rarely
+// pays for its merge: the vision shape is best in 2 parts, 32 x 2048^2
+// causal unsplit; tiny grids still split), f32 512 (its 32-key tiles of
+// 64 MFMAs keep a block busy: 12 x 1024^2 D 64 53 us in 6 parts vs 59 in
+// 2 and 103 unsplit; 4 x 16 x 512^2, 256 blocks, is best unsplit). Items
+// beyond kMaxFlashItems per (batch, head): descending query blocks, no
+// split.
 struct FlashPlan {
     bool flash = false;
     bool wide = false;
@@ -961,7 +964,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
-    p.wide = ((sh.q_len + 127) / 128) * bhs >= 512;
+    p.wide = ((sh.q_len + 127) / 128) * bhs >= 64;
     p.bm = p.wide ? 128 : 64;
     p.tk = f32 ? 32 : 64;
     p.qblocks = (uint32_t)((sh.q_len + p.bm - 1) / p.bm);
@@ -976,7 +979,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
-        const uint64_t slots = f32 ? 2048 : 256;
+        const uint64_t slots = f32 ? 512 : 128;
         const uint64_t target = (total + slots - 1) / slots;
         p.split_tiles = (uint32_t)(target > kMinPartTiles ? target : kMinPartTiles);
     }

@@ -34,6 +34,9 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (1, 2, 1, 40, 2048, 128, 128),  # MFMA path, key range split over 8 blocks
     (2, 3, 3, 100, 1500, 64, 64),   # MFMA path, key range split in 6 (f16) / 8 (f32, uneven) parts
     (1, 2, 2, 600, 600, 64, 64),    # MFMA path, causal: long query blocks split, short ones whole
+    (1, 64, 8, 130, 150, 64, 64),   # 128-query blocks (>= 64 of them): ragged query and key tiles
+    (1, 32, 4, 256, 300, 128, 128), # 128-query blocks at D 128, 8 q-heads per kv head
+    (1, 64, 16, 128, 1024, 64, 64), # 128-query blocks with split key ranges
 ]
 
 
