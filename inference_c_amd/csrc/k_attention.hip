@@ -928,11 +928,14 @@ hipError_t launch_sdpa(const S *q, const S *k, const S *v, const S *mask, S *out
 
 namespace {
 
-// Flash path choice for a shape: 128-query blocks (4 waves sharing each K/V
-// tile) when there are at least 64 of them, else 64-query blocks (measured:
+// Flash path choice for a shape: f16 256-query blocks (8 waves sharing each
+// K/V tile) when there are at least 256 of them (32 x 2048^2 D 128 82.8 us
+// vs 89.2 with 128-query blocks, 4096^2 causal 164.6 vs 179.9; 4 x 16 x
+// 512^2, 128 such blocks, 23.5 vs 20.9), else 128-query blocks (4 waves)
+// when there are at least 64 of them, else 64-query blocks (measured:
 // 12 x 1024^2 D 64 f16 20.1 us wide vs 22.2 narrow, 4 x 16 x 512^2 D 128
 // 21.1 vs 25.6, 32 x 1024^2 causal 33.2 vs 39.0, f32 4 x 16 x 512^2 56.6
-// vs 70.6). The work is then cut into items and ordered longest first.
+// vs 70.6; f32 stays at 128). The work is then cut into items and ordered longest first.
 // With a workspace, query blocks whose key range is long against the whole
 // launch are split: target split_tiles = max(total key tiles / slots,
 // kMinPartTiles), slots measured over 128 .. 3072: f16 128 (a split rarely
@@ -944,8 +947,7 @@ namespace {
 // split.
 struct FlashPlan {
     bool flash = false;
-    bool wide = false;
-    uint32_t bm = 64, tk = 64;
+    uint32_t bm = 64, tk = 64;   // queries per block (64, 128, or 256 for f16), keys per tile
     uint32_t qblocks = 0, items = 0;
     uint32_t split_tiles = 0;
     uint32_t max_parts = 1;
@@ -964,8 +966,9 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
-    p.wide = ((sh.q_len + 127) / 128) * bhs >= 64;
-    p.bm = p.wide ? 128 : 64;
+    if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
+    else if (((sh.q_len + 127) / 128) * bhs >= 64) p.bm = 128;
+    else p.bm = 64;
     p.tk = f32 ? 32 : 64;
     p.qblocks = (uint32_t)((sh.q_len + p.bm - 1) / p.bm);
     p.items = p.qblocks;
@@ -1084,11 +1087,21 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
 #define ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O)                                                  \
     do {                                                                                           \
         if (shape.head_dim == 64) {                                                                \
-            if (plan.wide) ICSDK_FLASH_VARIANTS(KERNEL, 64, 128, Q, K, V, M, O);                   \
+            if (plan.bm == 128) ICSDK_FLASH_VARIANTS(KERNEL, 64, 128, Q, K, V, M, O);              \
             else ICSDK_FLASH_VARIANTS(KERNEL, 64, 64, Q, K, V, M, O);                              \
         } else {                                                                                   \
-            if (plan.wide) ICSDK_FLASH_VARIANTS(KERNEL, 128, 128, Q, K, V, M, O);                  \
+            if (plan.bm == 128) ICSDK_FLASH_VARIANTS(KERNEL, 128, 128, Q, K, V, M, O);             \
             else ICSDK_FLASH_VARIANTS(KERNEL, 128, 64, Q, K, V, M, O);                             \
+        }                                                                                          \
+    } while (0)
+// the same with 256-query blocks (f16 only)
+#define ICSDK_FLASH_SHAPES_256(KERNEL, Q, K, V, M, O)                                              \
+    do {                                                                                           \
+        if (plan.bm == 256) {                                                                      \
+            if (shape.head_dim == 64) ICSDK_FLASH_VARIANTS(KERNEL, 64, 256, Q, K, V, M, O);        \
+            else ICSDK_FLASH_VARIANTS(KERNEL, 128, 256, Q, K, V, M, O);                            \
+        } else {                                                                                   \
+            ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O);                                             \
         }                                                                                          \
     } while (0)
 
@@ -1108,7 +1121,7 @@ hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float 
     const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace);
     const bool split = plan.max_parts > 1;
     const bool general = mask != nullptr;
-    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(plan.wide ? 256 : 128);
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm);
     ICSDK_FLASH_SHAPES(sdpa_flash_f32_kernel, q, k, v, mask, out);
     const hipError_t status = hipGetLastError();
     return status != hipSuccess || !split ? status : combine_splits(a, plan, out, s);
@@ -1128,14 +1141,15 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     // the raw-product softmax needs scale > 0; other scales take the general
     // (mask) variant, whose mask may be null
     const bool general = mask != nullptr || !(scale > 0.0f);
-    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(plan.wide ? 256 : 128);
-    ICSDK_FLASH_SHAPES(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm);
+    ICSDK_FLASH_SHAPES_256(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
     const hipError_t status = hipGetLastError();
     return status != hipSuccess || !split ? status : combine_splits(a, plan, o16, s);
 }
 
 }  // namespace k
 
+#undef ICSDK_FLASH_SHAPES_256
 #undef ICSDK_FLASH_SHAPES
 #undef ICSDK_FLASH_VARIANTS
 

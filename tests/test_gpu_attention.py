@@ -37,6 +37,8 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (1, 64, 8, 130, 150, 64, 64),   # 128-query blocks (>= 64 of them): ragged query and key tiles
     (1, 32, 4, 256, 300, 128, 128), # 128-query blocks at D 128, 8 q-heads per kv head
     (1, 64, 16, 128, 1024, 64, 64), # 128-query blocks with split key ranges
+    (2, 64, 8, 257, 100, 64, 64),   # f16 256-query blocks (>= 256 of them), ragged; f32 128
+    (1, 128, 32, 300, 90, 128, 128),  # f16 256-query blocks at D 128
 ]
 
 
