@@ -75,7 +75,7 @@ class Hip:
         assert self.lib.hipMemsetAsync(ptr, 0, nbytes, stream) == 0
 
 
-TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "cfg2_and_q8_gemv_hbm_traffic.md")
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "tensor_ops_hbm_traffic.md")
 
 
 def measured_traffic(kernel):
@@ -428,6 +428,42 @@ def pmc_probe(sdk, reps=3):
     del packed
     ops.append(("linear_q8_0_f16_1x8192_to_28672",
                 lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
+    # the configs[2..4] kernels at their BASELINE shapes
+    t["x3"], t["y3"] = sdk.tensor("f16", (16384, 2048)), sdk.tensor("f16", (16384, 2048))
+    t["w3"] = sdk.tensor("f16", (2048,))
+    sdk.call("tensor_fill_normal", t["x3"], 3, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_uniform", t["w3"], 3, 1, 0.5, 1.5)
+    ops.append(("cfg3_rms_norm_f16", lambda: sdk.call("tensor_rms_norm_f16", t["x3"], t["w3"],
+                                                      1e-6, t["y3"])))
+    t["lg"], t["sm"] = sdk.tensor("f16", (32, 2048, 2048)), sdk.tensor("f16", (32, 2048, 2048))
+    t["rs"] = sdk.tensor("f32", (32, 2048))
+    sdk.call("tensor_fill_normal", t["lg"], 3, 2, 0.0, 3.0)
+    ops.append(("cfg3_causal_softmax_f16", lambda: sdk.call("tensor_softmax_f16", t["lg"], 1,
+                                                            t["sm"])))
+    ops.append(("cfg3_row_sum_f16", lambda: sdk.call("tensor_row_sum_f16", t["lg"], t["rs"])))
+    ops.append(("cfg3_row_max_f16", lambda: sdk.call("tensor_row_max_f16", t["lg"], t["rs"])))
+    B, S, H, D = 16, 1024, 32, 64
+    perm = TensorView.make((B, H, S, D), (S * H * D, D, H * D, 1), 0)
+    t["x4"], t["o4"] = sdk.tensor("f16", (B, S, H, D)), sdk.tensor("f16", (B, H, S, D))
+    t["a4"], t["m4"] = sdk.tensor("f16", (1, H, 1, D)), sdk.tensor("f16", (B, 1, S, 1))
+    sdk.call("tensor_fill_normal", t["x4"], 4, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_uniform", t["a4"], 4, 1, -1.0, 1.0)
+    sdk.call("tensor_fill_uniform", t["m4"], 4, 2, -1.0, 1.0)
+    ops.append(("cfg4_permuted_broadcast_f16", lambda: sdk.call(
+        "tensor_view_add_mul_f16", t["x4"], perm, t["a4"], t["m4"], t["o4"])))
+    t["x5"], t["r5"] = sdk.tensor("f16", (4096, 2048)), sdk.tensor("f16", (4096, 2048))
+    t["h5"], t["n5"] = sdk.tensor("f16", (4096, 2048)), sdk.tensor("f16", (4096, 2048))
+    sdk.call("tensor_fill_normal", t["x5"], 5, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", t["r5"], 5, 1, 0.0, 1.0)
+    ops.append(("cfg5_residual_rms_norm_f16", lambda: sdk.call(
+        "tensor_residual_rms_norm_f16", t["x5"], t["r5"], t["w3"], 1e-6, t["h5"], t["n5"])))
+    vocab, width, tokens = 32000, 2048, 32768
+    t["emb"], t["eo"] = sdk.tensor("f16", (vocab, width)), sdk.tensor("f16", (tokens, width))
+    sdk.call("tensor_fill_normal", t["emb"], 6, 0, 0.0, 1.0)
+    t["ids"] = sdk.tensor("i32", (tokens,)).upload(
+        ((np.arange(tokens, dtype=np.int64) * 2654435761) % vocab).astype(np.int32))
+    ops.append(("embedding_lookup_f16", lambda: sdk.call("tensor_embedding_lookup_f16", t["emb"],
+                                                         t["ids"], t["eo"])))
     # kernels that stage data in LDS, for the LDS instruction / bank-conflict
     # pass: RoPE (angle table), a [4096, 4096] f16 transpose (64x64 tiles),
     # the global sum/max (cross-wave combine) and flash attention f16 / f32
