@@ -5,15 +5,17 @@
 // 16-byte aligned tensors): one kernel. The host computes the pair
 // denominators pow(theta, 2d/dim) in double with the C library's pow, as the
 // reference does, and passes them as kernel arguments. A block covers whole
-// positions: each lane first issues the loads of its (head row, chunk)
-// items -- the left vector (pairs d..d+E-1) and the right vector (pairs
-// d+half..) of the row, both streamed -- then a few lanes compute the
-// block's rotations, angle = (float)((double)(offset + p) / denom[d]) and
-// sincosf, into LDS, and after one barrier every lane rotates its pairs in
-// f32 (left*c - right*s, right*c + left*s, no contraction) and stores both
-// vectors, written through L2 into the bytes they came from. Every q/k byte
-// is read once and written once; the angles cost `half` sincos per position,
-// shared by all heads of the position.
+// positions: each lane pair first issues the loads of its (head row, chunk)
+// items -- one lane the left vector (pairs d..d+E-1), its partner 32 lanes
+// away the right vector (pairs d+half..), both streamed, so a wave's load
+// covers whole contiguous rows -- then a few lanes compute the block's
+// rotations, angle = (float)((double)(offset + p) / denom[d]) and sincosf,
+// into LDS, and after one barrier the pair exchanges its vectors across the
+// wave halves, every lane rotates its side's pairs in f32 (left*c - right*s,
+// right*c + left*s, no contraction) and stores its vector, written through
+// L2 into the bytes it came from. Every q/k byte is read once and written
+// once; the angles cost `half` sincos per position, shared by all heads of
+// the position.
 //
 // Table path (other shapes): a table kernel computes the same (cos, sin) per
 // (position, pair) into device scratch, then one lane per pair rotates.
@@ -94,12 +96,26 @@ struct RopeDenoms {
 
 // Item = (position, row, chunk): row < qh is a q head, else a k head; chunk
 // c covers pairs c*E .. c*E+E-1. Items are numbered position-major; block
-// (x, y) owns items y*kIt*kBlock .. +kIt*kBlock of positions x*ppb ..
-// x*ppb+ppb-1 and computes those positions' rotations. A lane handles kIt
-// items; its loads are issued unconditionally (a lane past the end re-reads
-// item 0, which lane 0 loads anyway) so that no branch makes it wait for one
-// item before requesting the next, and there is no loop, so nothing waits
-// for the loads before the rotations are computed.
+// (x, y) owns items y*kIt*128 .. +kIt*128 of positions x*ppb ..
+// x*ppb+ppb-1 and computes those positions' rotations.
+//
+// Lanes l and l + 32 of a wave share an item: lane l < 32 moves the item's
+// left vector, lane l + 32 its right vector (half elements further on). A
+// wave's 32 items are consecutive, so each of its load and store
+// instructions covers whole rows -- 32 / kChunks rows of 2 * half elements,
+// one contiguous run -- instead of the left (or right) halves of twice as
+// many rows. One v_permlane32_swap per dword then gives every lane both
+// vectors (lanes 0-31 keep theirs in the first result and receive lane + 32's
+// in the second; lanes 32-63 receive lane - 32's in the first and keep theirs
+// in the second, so in every lane the first result is the left vector and the
+// second the right one), and each lane writes its own side:
+// left' = l*c + r*(-s) (== l*c - r*s exactly), right' = r*c + l*s.
+// A lane handles kIt items; its loads are issued unconditionally (a lane
+// past the end re-reads item 0, which lane 0 loads anyway) so that no branch
+// makes it wait for one item before requesting the next, and there is no
+// loop, so nothing waits for the loads before the rotations are computed.
+constexpr uint32_t kPairItems = kBlock / 2;   // items per block and per kIt
+
 template <typename S, int kChunks, int kIt>
 __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S *__restrict__ k,
                                                             uint32_t seq, uint32_t qh,
@@ -114,9 +130,11 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     const uint32_t npos = min(ppb, seq - p0);
     const uint32_t items = npos * per_pos;
     const uint32_t rot_entries = npos * half;
-    const uint32_t it0 = blockIdx.y * (uint32_t)(kIt * kBlock);
-    Vec16<S> lv[kIt], rv[kIt];
-    uint32_t off[kIt];   // element offset of the item's left vector in its q / k window
+    const uint32_t it0 = blockIdx.y * (uint32_t)(kIt * kPairItems);
+    const uint32_t lane = threadIdx.x & (kWave - 1), side = lane >> 5;
+    const uint32_t wave = threadIdx.x / kWave;
+    Vec16<S> v[kIt];
+    uint32_t off[kIt];   // element offset of the lane's vector in its q / k window
     bool in_q[kIt];
     uint32_t slot[kIt];  // index of the item's first rotation in `rot`
     bool ok[kIt];
@@ -125,7 +143,7 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     S *const k0 = k + (size_t)p0 * kh * (2 * half);
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
-        const uint32_t raw = it0 + threadIdx.x + u * kBlock;
+        const uint32_t raw = it0 + (u * (kBlock / kWave) + wave) * 32 + (lane & 31);
         ok[u] = raw < items;
         const uint32_t item = ok[u] ? raw : 0u;
         const uint32_t pp = item / per_pos;
@@ -133,11 +151,10 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         const uint32_t row = rest / kChunks;
         const uint32_t c = rest - row * kChunks;
         in_q[u] = row < qh;
-        off[u] = (in_q[u] ? pp * qh + row : pp * kh + (row - qh)) * (2 * half) + c * E;
+        off[u] = (in_q[u] ? pp * qh + row : pp * kh + (row - qh)) * (2 * half) + c * E +
+                 side * half;
         slot[u] = pp * half + c * E;
-        const S *src = (in_q[u] ? q0 : k0) + off[u];
-        lv[u] = load16_stream(src);
-        rv[u] = load16_stream(src + half);
+        v[u] = load16_stream((in_q[u] ? q0 : k0) + off[u]);
     }
     // The denominators go to LDS through scalar loads (uniform addresses,
     // counted by lgkmcnt), so computing the rotations never waits for the
@@ -161,14 +178,26 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     const OutWindow k_out(k0, npos * kh * (2 * half) * (uint32_t)sizeof(S));
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
+        // every lane takes part in the swap (a lane past the end holds item 0)
+        const uint4 words = __builtin_bit_cast(uint4, v[u]);
+        const uint32_t w[4] = {words.x, words.y, words.z, words.w};
+        uint32_t lw[4], rw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const auto r = __builtin_amdgcn_permlane32_swap(w[j], w[j], false, false);
+            lw[j] = r[0];
+            rw[j] = r[1];
+        }
         if (!ok[u]) continue;
-        Vec16<S> lo, ro;
+        const Vec16<S> lv = __builtin_bit_cast(Vec16<S>, uint4{lw[0], lw[1], lw[2], lw[3]});
+        const Vec16<S> rv = __builtin_bit_cast(Vec16<S>, uint4{rw[0], rw[1], rw[2], rw[3]});
+        Vec16<S> out;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const float2 t = rot[slot[u] + e];
-            const float l = Elem<S>::load(lv[u].v[e]), r = Elem<S>::load(rv[u].v[e]);
-            lo.v[e] = Elem<S>::store(l * t.x - r * t.y);
-            ro.v[e] = Elem<S>::store(r * t.x + l * t.y);
+            const float l = Elem<S>::load(lv.v[e]), r = Elem<S>::load(rv.v[e]);
+            const float a = side ? r : l, b = side ? l : r, sb = side ? t.y : -t.y;
+            out.v[e] = Elem<S>::store(a * t.x + b * sb);
         }
         // The window is chosen per wave (a descriptor must be wave-uniform):
         // a wave whose items all lie in q, or all in k, writes through its
@@ -177,15 +206,11 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         const uint64_t active = __builtin_amdgcn_ballot_w64(true);
         const uint64_t q_lanes = __builtin_amdgcn_ballot_w64(in_q[u]);
         if (q_lanes == active) {
-            q_out.store16(bytes, lo);
-            q_out.store16(bytes + half * (uint32_t)sizeof(S), ro);
+            q_out.store16(bytes, out);
         } else if (q_lanes == 0) {
-            k_out.store16(bytes, lo);
-            k_out.store16(bytes + half * (uint32_t)sizeof(S), ro);
+            k_out.store16(bytes, out);
         } else {
-            S *dst = (in_q[u] ? q0 : k0) + off[u];
-            store16_stream(dst, lo);
-            store16_stream(dst + half, ro);
+            store16_stream((in_q[u] ? q0 : k0) + off[u], out);
         }
     }
 }
@@ -220,18 +245,22 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
         RopeDenoms denom{};
         for (size_t d = 0; d < half; ++d)
             denom.d[d] = std::pow(theta, (2.0 * (double)d) / (double)dim);
-        // whole positions per block: about one item per lane, and at most
-        // kLdsPairs rotations
+        // whole positions per block: up to kTargetIt items per lane pair
+        // (the loads of 8 items in flight per lane measured fastest at the
+        // BASELINE shape: 4 positions of 64 rows x 4 chunks, 14.4 -> 13.0 us),
+        // and at most kLdsPairs rotations
+        constexpr size_t kTargetIt = 8;
         const size_t per_pos = heads * chunks;
-        size_t ppb = per_pos >= (size_t)kBlock ? 1 : (size_t)kBlock / per_pos;
+        size_t ppb = per_pos >= kTargetIt * kPairItems ? 1 : kTargetIt * kPairItems / per_pos;
         if (ppb * half > (size_t)kLdsPairs) ppb = (size_t)kLdsPairs / half;
+        if (ppb > seq) ppb = seq;
         if (ppb < 1) ppb = 1;
         const uint32_t a = (uint32_t)seq, b = (uint32_t)qh, c = (uint32_t)kh, d = (uint32_t)ppb;
-        // items per lane: 1, 2 or 4; positions with more items than 4 per
+        // items per lane: 1, 2, 4 or 8; positions with more items than 8 per
         // lane are split over blockIdx.y
-        const size_t lanes_needed = (ppb * per_pos + kBlock - 1) / kBlock;
-        const int it = lanes_needed <= 1 ? 1 : lanes_needed <= 2 ? 2 : 4;
-        const size_t splits = (ppb * per_pos + (size_t)it * kBlock - 1) / ((size_t)it * kBlock);
+        const size_t pairs_needed = (ppb * per_pos + kPairItems - 1) / kPairItems;
+        const int it = pairs_needed <= 1 ? 1 : pairs_needed <= 2 ? 2 : pairs_needed <= 4 ? 4 : 8;
+        const size_t splits = (ppb * per_pos + (size_t)it * kPairItems - 1) / ((size_t)it * kPairItems);
         const dim3 grid((unsigned)((seq + ppb - 1) / ppb), (unsigned)splits), block(kBlock);
         const size_t lds = ppb * half * sizeof(float2);
 #define ICSDK_ROPE(CH, IT)                                                                      \
@@ -241,7 +270,8 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
     do {                                                                                        \
         if (it == 1) ICSDK_ROPE(CH, 1);                                                         \
         else if (it == 2) ICSDK_ROPE(CH, 2);                                                    \
-        else ICSDK_ROPE(CH, 4);                                                                 \
+        else if (it == 4) ICSDK_ROPE(CH, 4);                                                    \
+        else ICSDK_ROPE(CH, 8);                                                                 \
     } while (0)
         switch (chunks) {
             case 1: ICSDK_ROPE_IT(1); break;

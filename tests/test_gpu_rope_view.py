@@ -16,7 +16,10 @@ F16 = np.float16
 @pytest.mark.parametrize("device", [True, False])
 @pytest.mark.parametrize("seq,qh,kh,dim,offset", [
     (4096, 32, 32, 64, 0), (17, 8, 2, 128, 5), (3, 1, 1, 2, 0), (9, 3, 5, 6, 1000),
-    (5, 2, 2, 256, 123456)])
+    (5, 2, 2, 256, 123456),
+    # fused path: waves straddling the q/k rows, a ragged last block, and
+    # positions of more than 1024 (row, chunk) items split over blocks
+    (33, 5, 3, 64, 7), (3, 200, 100, 64, 0), (70, 1, 1, 16, 2)])
 def test_rope_f16(sdk, orc, seq, qh, kh, dim, offset, device):
     q = orc.normal((seq, qh, dim), 50, 0, 0.0, 1.0)
     k = orc.normal((seq, kh, dim), 50, 1, 0.0, 1.0)
@@ -27,7 +30,8 @@ def test_rope_f16(sdk, orc, seq, qh, kh, dim, offset, device):
     rope_close(tk.download(), wk, k)
 
 
-@pytest.mark.parametrize("seq,qh,kh,dim,offset", [(64, 4, 2, 64, 0), (7, 3, 3, 10, 77)])
+@pytest.mark.parametrize("seq,qh,kh,dim,offset", [(64, 4, 2, 64, 0), (7, 3, 3, 10, 77),
+                                                   (2, 150, 150, 64, 3), (45, 3, 1, 8, 9)])
 def test_rope_f32(sdk, orc, seq, qh, kh, dim, offset):
     q = orc.normal((seq, qh, dim), 51, 0, 0.0, 1.0, "f32")
     k = orc.normal((seq, kh, dim), 51, 1, 0.0, 1.0, "f32")
