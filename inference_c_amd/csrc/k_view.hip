@@ -170,6 +170,95 @@ __global__ __launch_bounds__(kBlock) void view_gather_kernel(const S *__restrict
     window.store16(threadIdx.x * 16u, out);
 }
 
+// Short gather: the common views -- at most two outer dims, whole blocks of
+// kBlock vectors per inner plane, a power-of-two number of vectors per row,
+// and every element offset below 2^32. The outer coordinates are blockIdx.z
+// and blockIdx.y (a 3-D grid), strides are 32-bit, the row split is a shift
+// and there is no bounds test: a wave reaches its loads after a few
+// independent scalar loads instead of the general plan's chain of dependent
+// ones (config-4 shape, measured in isolation: 23.6 -> 22.7 us).
+struct ShortPlan {
+    uint32_t ox[2], oa[2], om[2];  // element strides of the outer dims (grid z, y)
+    uint32_t x_offset;
+    uint32_t vecs_log2;            // log2(vectors per row)
+    uint32_t row_x, row_a, row_m;  // element strides of the row dim
+};
+
+template <typename S, int kA, int kM>
+__global__ __launch_bounds__(kBlock) void view_gather_short_kernel(const S *__restrict__ x,
+                                                                   const S *__restrict__ addend,
+                                                                   const S *__restrict__ mult,
+                                                                   S *__restrict__ y,
+                                                                   ShortPlan plan) {
+    constexpr int E = Vec16<S>::N;
+    const uint32_t xb = plan.x_offset + blockIdx.z * plan.ox[0] + blockIdx.y * plan.ox[1];
+    const uint32_t ab = blockIdx.z * plan.oa[0] + blockIdx.y * plan.oa[1];
+    const uint32_t mb = blockIdx.z * plan.om[0] + blockIdx.y * plan.om[1];
+    const uint32_t plane_vec0 = blockIdx.x * kBlock;
+    const size_t out_vec0 = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * (gridDim.x * kBlock) +
+                            plane_vec0;
+    const uint32_t t = plane_vec0 + threadIdx.x;
+    const uint32_t row = t >> plan.vecs_log2;
+    const uint32_t vec = t - (row << plan.vecs_log2);
+    const Vec16<S> xv = load16_stream(x + (xb + row * plan.row_x + vec * E));
+    Vec16<S> av, mv;
+    float a_scalar = 0.0f, m_scalar = 1.0f;
+    if constexpr (kA == kVector) av = load16(addend + (ab + row * plan.row_a + vec * E));
+    if constexpr (kA == kScalar) a_scalar = Elem<S>::load(addend[ab + row * plan.row_a]);
+    if constexpr (kM == kVector) mv = load16(mult + (mb + row * plan.row_m + vec * E));
+    if constexpr (kM == kScalar) m_scalar = Elem<S>::load(mult[mb + row * plan.row_m]);
+    Vec16<S> out;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        float r = Elem<S>::load(xv.v[e]);
+        if constexpr (kA != kNone) r = r + (kA == kVector ? Elem<S>::load(av.v[e]) : a_scalar);
+        if constexpr (kM != kNone) r = r * (kM == kVector ? Elem<S>::load(mv.v[e]) : m_scalar);
+        out.v[e] = Elem<S>::store(r);
+    }
+    const OutWindow window(y + out_vec0 * E, kBlock * 16u);
+    window.store16(threadIdx.x * 16u, out);
+}
+
+// The short plan of a view the gather path takes, or false when the view
+// needs the general kernel.
+template <typename S>
+bool short_plan(const Coalesced &c, uint64_t x_offset, uint64_t n, ShortPlan *plan, dim3 *grid) {
+    constexpr uint64_t E = Vec16<S>::N;
+    const int last = c.rank - 1;
+    const int outer_rank = c.rank >= 2 ? c.rank - 2 : 0;
+    if (outer_rank > 2 || n > 0xffffffffull) return false;
+    const uint64_t vecs = c.shape[last] / E;
+    const uint64_t rows = c.rank >= 2 ? c.shape[last - 1] : 1;
+    const uint64_t plane = rows * vecs;
+    if ((vecs & (vecs - 1)) != 0 || plane % kBlock != 0 || plane / kBlock > 0x7fffffffull)
+        return false;
+    uint64_t ext[2] = {1, 1}, ox[2] = {0, 0}, oa[2] = {0, 0}, om[2] = {0, 0};
+    for (int d = 0; d < outer_rank; ++d) {
+        const int slot = 2 - outer_rank + d;
+        ext[slot] = c.shape[d];
+        ox[slot] = (uint64_t)c.x_stride[d];
+        oa[slot] = c.a_stride[d];
+        om[slot] = c.m_stride[d];
+    }
+    if (ext[0] > 65535 || ext[1] > 65535) return false;
+    const uint64_t row_x = c.rank >= 2 ? (uint64_t)c.x_stride[last - 1] : 0;
+    const uint64_t row_a = c.rank >= 2 ? c.a_stride[last - 1] : 0;
+    const uint64_t row_m = c.rank >= 2 ? c.m_stride[last - 1] : 0;
+    // the largest element offset each operand is addressed at, in 32 bits
+    auto reach = [&](uint64_t base, const uint64_t (&o)[2], uint64_t row, uint64_t inner) {
+        return base + (ext[0] - 1) * o[0] + (ext[1] - 1) * o[1] + (rows - 1) * row + inner;
+    };
+    if (reach(x_offset, ox, row_x, vecs * E) > 0xffffffffull ||
+        reach(0, oa, row_a, vecs * E) > 0xffffffffull || reach(0, om, row_m, vecs * E) > 0xffffffffull)
+        return false;
+    *plan = ShortPlan{{(uint32_t)ox[0], (uint32_t)ox[1]}, {(uint32_t)oa[0], (uint32_t)oa[1]},
+                      {(uint32_t)om[0], (uint32_t)om[1]}, (uint32_t)x_offset,
+                      (uint32_t)__builtin_ctzll(vecs), (uint32_t)row_x, (uint32_t)row_a,
+                      (uint32_t)row_m};
+    *grid = dim3((unsigned)(plane / kBlock), (unsigned)ext[1], (unsigned)ext[0]);
+    return true;
+}
+
 // ---- scalar path -------------------------------------------------------------
 
 struct ScalarPlan {
@@ -347,9 +436,19 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
         gather_plan<S>(c, v.offset, n, addend != nullptr, mult != nullptr, &gp, &blocks)) {
         const int ka = !addend ? kNone : c.a_stride[last] != 0 ? kVector : kScalar;
         const int km = !mult ? kNone : c.m_stride[last] != 0 ? kVector : kScalar;
+        ShortPlan sp;
+        dim3 short_grid;
+        const bool use_short = short_plan<S>(c, v.offset, n, &sp, &short_grid);
         const dim3 grid(blocks), block(kBlock);
 #define ICSDK_GATHER(A, M)                                                                      \
-    hipLaunchKernelGGL((view_gather_kernel<S, A, M>), grid, block, 0, s, x, addend, mult, y, gp)
+    do {                                                                                        \
+        if (use_short)                                                                          \
+            hipLaunchKernelGGL((view_gather_short_kernel<S, A, M>), short_grid, block, 0, s, x,  \
+                               addend, mult, y, sp);                                            \
+        else                                                                                    \
+            hipLaunchKernelGGL((view_gather_kernel<S, A, M>), grid, block, 0, s, x, addend,     \
+                               mult, y, gp);                                                    \
+    } while (0)
         switch (ka * 3 + km) {
             case 0: ICSDK_GATHER(kNone, kNone); break;
             case 1: ICSDK_GATHER(kNone, kVector); break;

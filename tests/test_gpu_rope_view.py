@@ -87,7 +87,8 @@ def test_config4_permuted_broadcast(sdk, orc, device):
 
 @pytest.mark.parametrize("case", ["vector_tile", "vector_tile_ragged", "vector_rows", "tile",
                                   "scalar", "broadcast_x", "offset", "rank1", "coalesce_contig",
-                                  "rank6", "unit_dims", "one_vector_runs", "addend_inner_bcast"])
+                                  "rank6", "unit_dims", "one_vector_runs", "addend_inner_bcast",
+                                  "short_rank4", "short_rank3_offset", "short_rank2"])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_view_paths(sdk, orc, case, dtype):
     dt = "f16" if dtype == "f16" else "f32"
@@ -159,6 +160,22 @@ def test_view_paths(sdk, orc, case, dtype):
         shape, strides, off = (4, 6, 32), (32, 128, 1), 0
         A = orc.uniform((4, 6, 1), 64, 1, -1, 1, dt)
         M = orc.uniform((1, 6, 32), 64, 2, -1, 1, dt)
+    # the short gather kernel: <= 2 outer dims, whole 256-vector blocks per
+    # plane, a power-of-two number of vectors per row
+    elif case == "short_rank4":  # (0,2,1,3) permutation, vector addend, scalar multiplier
+        x = orc.normal((2, 64, 3, 64), 65, 0, 0.0, 1.0, dt)
+        shape, strides, off = (2, 3, 64, 64), (64 * 3 * 64, 64, 3 * 64, 1), 0
+        A = orc.uniform((1, 3, 1, 64), 65, 1, -1, 1, dt)
+        M = orc.uniform((2, 1, 64, 1), 65, 2, -1, 1, dt)
+    elif case == "short_rank3_offset":  # sliced rows at an offset, scalar addend, vector multiplier
+        x = orc.normal((4, 130, 32), 66, 0, 0.0, 1.0, dt)
+        shape, strides, off = (3, 128, 32), (130 * 32, 32, 1), 2 * 32
+        A = orc.uniform((1, 128, 1), 66, 1, -1, 1, dt)
+        M = orc.uniform((3, 1, 32), 66, 2, -1, 1, dt)
+    elif case == "short_rank2":  # strided rows, no outer dims
+        x = orc.normal((300, 128), 67, 0, 0.0, 1.0, dt)
+        shape, strides, off = (256, 64), (128, 1), 64
+        A, M = orc.uniform((256, 1), 67, 1, -1, 1, dt), None
     else:
         x = orc.normal((100,), 57, 0, 0.0, 1.0, dt)
         shape, strides, off = (33,), (3,), 1
