@@ -346,7 +346,13 @@ __device__ inline void write_partial(const SdpaArgs &a, uint32_t split, size_t r
 // otherwise out = (sum_s w_s o_s) * (1 / sum_s w_s l_s) with w_s =
 // exp(m_s - M) (exp2 when the maxima are in log2 units). One thread per 8
 // output elements (dim % 8 == 0 on the flash path).
-template <typename S, bool kLog2>
+//
+// kParts >= the launch's largest part count: every part's (m, l) and output
+// vectors are requested up front, unconditionally (a part index past the
+// row's own count reads its last part again, which stays in bounds, and is
+// left out of the sums), so a row costs one memory round trip; walking the
+// parts in a run-time loop waited for each part's loads in turn.
+template <typename S, bool kLog2, int kParts>
 __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__restrict__ out,
                                                               uint32_t bm, uint32_t tk,
                                                               uint32_t first_row) {
@@ -361,27 +367,37 @@ __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__r
     const size_t row = srow / suffix * a.ql + qi;
     const uint32_t splits = split_parts(
         flash_tiles(a.ql, a.kl, a.causal != 0, a.causal_offset, bm, tk, qi / bm), a.split_tiles);
+    f32x4 ml[kParts], po_lo[kParts], po_hi[kParts];
+#pragma unroll
+    for (int s = 0; s < kParts; ++s) {
+        const size_t part = (size_t)min((uint32_t)s, splits - 1) * rows + row;
+        ml[s] = a.part_ml[part];
+        const f32x4 *po = reinterpret_cast<const f32x4 *>(a.part_o + part * a.dim + 8 * g);
+        po_lo[s] = po[0];
+        po_hi[s] = po[1];
+    }
     float big = -__builtin_inff();
     bool nan_flag = false;
-    for (uint32_t s = 0; s < splits; ++s) {
-        const f32x4 ml = a.part_ml[(size_t)s * rows + row];
-        big = fmaxf(big, ml.x);
-        nan_flag = nan_flag || ml.z != 0.0f;
+#pragma unroll
+    for (int s = 0; s < kParts; ++s) {
+        if ((uint32_t)s < splits) {
+            big = fmaxf(big, ml[s].x);
+            nan_flag = nan_flag || ml[s].z != 0.0f;
+        }
     }
     f32x4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
     float total = 0.0f;
     if (__builtin_isfinite(big)) {
-        for (uint32_t s = 0; s < splits; ++s) {
-            const f32x4 ml = a.part_ml[(size_t)s * rows + row];
+#pragma unroll
+        for (int s = 0; s < kParts; ++s) {
+            if ((uint32_t)s >= splits) continue;
             // a part that saw no visible key has sum 0 and output 0; every
             // other part is added even at weight 0, so a NaN it holds stays
-            const float w = ml.x == -__builtin_inff() ? 0.0f
-                            : kLog2 ? __builtin_amdgcn_exp2f(ml.x - big) : expf(ml.x - big);
-            const f32x4 *po = reinterpret_cast<const f32x4 *>(
-                a.part_o + ((size_t)s * rows + row) * a.dim + 8 * g);
-            total += w * ml.y;
-            lo += w * po[0];
-            hi += w * po[1];
+            const float w = ml[s].x == -__builtin_inff() ? 0.0f
+                            : kLog2 ? __builtin_amdgcn_exp2f(ml[s].x - big) : expf(ml[s].x - big);
+            total += w * ml[s].y;
+            lo += w * po_lo[s];
+            hi += w * po_hi[s];
         }
     }
     const bool zero = !__builtin_isfinite(big);
@@ -1063,9 +1079,18 @@ template <typename S>
 hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStream_t s) {
     const uint32_t first_row = p.first_split * p.bm;
     const size_t n = (size_t)a.batch * a.qh * (a.ql - first_row) * (a.dim / 8);
-    hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2>),
-                       dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, a, out,
-                       p.bm, p.tk, first_row);
+    const dim3 grid((unsigned)((n + kBlock - 1) / kBlock)), block(kBlock);
+    // the part-count bucket: no row of this launch has more parts
+    static_assert(kMaxKeyParts <= 8, "combine buckets");
+    if (p.max_parts <= 2)
+        hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2, 2>), grid, block, 0, s, a, out,
+                           p.bm, p.tk, first_row);
+    else if (p.max_parts <= 4)
+        hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2, 4>), grid, block, 0, s, a, out,
+                           p.bm, p.tk, first_row);
+    else
+        hipLaunchKernelGGL((sdpa_combine_kernel<S, sizeof(S) == 2, 8>), grid, block, 0, s, a, out,
+                           p.bm, p.tk, first_row);
     return hipGetLastError();
 }
 
