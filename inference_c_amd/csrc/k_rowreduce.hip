@@ -150,9 +150,16 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
     using R = RowRegs<S, NV, WPR, kExact>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
-    if (slot.row >= rows) return;
+    // A slot past the last row recomputes the last row and stores nothing
+    // (its output windows are 0 bytes long: the hardware drops the stores):
+    // no branch waits for `rows` before the loads, so the kernel's argument
+    // loads return in one round trip (an early return cost three before the
+    // row's first load), and no branch on it lets the compiler sink the
+    // weight loads down to the stores.
+    const bool live = slot.row < rows;
+    const size_t row = live ? slot.row : rows - 1;
     const uint32_t vpr = width / E;
-    const size_t base = slot.row * width;
+    const size_t base = row * width;
     Vec16<S> wv[NV];
     load_params<S, NV, WPR, kExact>(w, slot.t, vpr, wv);
     __builtin_amdgcn_sched_barrier(0);
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             rv[j] = load16_stream(residual + base + (size_t)R::clamp(j, slot.t, vpr) * E);
-        const OutWindow sums(sum_out + base, row_bytes);
+        const OutWindow sums(sum_out + base, live ? row_bytes : 0u);
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const uint32_t vi = slot.t + j * R::T;
@@ -185,7 +192,7 @@ __global__ __launch_bounds__(kBlock) void rms_norm_kernel(
         for (int e = 0; e < E; ++e) squares += r.v[j][e] * r.v[j][e];
     squares = group_sum<WPR>(squares, lds);
     const float scale = 1.0f / sqrtf(squares / (float)width + eps);
-    const OutWindow out(y + base, row_bytes);
+    const OutWindow out(y + base, live ? row_bytes : 0u);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
