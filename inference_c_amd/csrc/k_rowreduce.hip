@@ -243,9 +243,12 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
     using R = RowRegs<S, NV, WPR, kExact>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
-    if (slot.row >= rows) return;
+    // past the last row: recompute the last row into a 0-byte window (as in
+    // rms_norm_kernel), so no branch waits for `rows` before the loads
+    const bool live = slot.row < rows;
+    const size_t row = live ? slot.row : rows - 1;
     const uint32_t vpr = width / E;
-    const size_t base = slot.row * width;
+    const size_t base = row * width;
     Vec16<S> sv[NV], bv[NV];
     if constexpr (kScale) load_params<S, NV, WPR, kExact>(scale, slot.t, vpr, sv);
     if constexpr (kBias) load_params<S, NV, WPR, kExact>(bias, slot.t, vpr, bv);
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(kBlock) void layer_norm_kernel(
         }
     variance = group_sum<WPR>(variance, lds);
     const float inverse_std = 1.0f / sqrtf(variance / (float)width + eps);
-    const OutWindow out(y + base, width * (uint32_t)sizeof(S));
+    const OutWindow out(y + base, live ? width * (uint32_t)sizeof(S) : 0u);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
@@ -335,11 +338,14 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     using R = RowRegs<S, NV, WPR>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
-    if (slot.row >= rows) return;
+    // past the last row: recompute the last row and store nothing, so no
+    // branch waits for `rows` before the loads
+    const bool live = slot.row < rows;
+    const size_t row = live ? slot.row : rows - 1;
     const uint32_t vpr = width / E;
-    const size_t base = slot.row * width;
+    const size_t base = row * width;
     // keys 0..limit are visible
-    const uint64_t limit = q_len ? (uint64_t)(slot.row % q_len) + causal_offset
+    const uint64_t limit = q_len ? (uint64_t)(row % q_len) + causal_offset
                                  : (uint64_t)width;
     const float neg_inf = -__builtin_inff();
     R r;
@@ -402,7 +408,7 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
-        if (vi < vpr) {
+        if (vi < vpr && live) {
             Vec16<S> out;
 #pragma unroll
             for (int e = 0; e < E; ++e) out.v[e] = Elem<S>::store(r.v[j][e]);
@@ -466,10 +472,13 @@ __global__ __launch_bounds__(kBlock) void row_reduce_kernel(const S *__restrict_
     using R = RowRegs<S, NV, WPR>;
     constexpr int E = R::E;
     const RowSlot<WPR> slot;
-    if (slot.row >= rows) return;
+    // past the last row: reduce the last row again and store nothing, so no
+    // branch waits for `rows` before the loads
+    const bool live = slot.row < rows;
+    const size_t row = live ? slot.row : rows - 1;
     const uint32_t vpr = width / E;
     R r;
-    r.load(x + slot.row * width, slot.t, vpr, kMax ? -__builtin_inff() : 0.0f);
+    r.load(x + row * width, slot.t, vpr, kMax ? -__builtin_inff() : 0.0f);
     float acc = kMax ? -__builtin_inff() : 0.0f;
     bool has_nan = false;
 #pragma unroll
@@ -491,7 +500,7 @@ __global__ __launch_bounds__(kBlock) void row_reduce_kernel(const S *__restrict_
     } else {
         result = group_sum<WPR>(acc, lds);
     }
-    if (slot.t == 0) y[slot.row] = result;
+    if (slot.t == 0 && live) y[row] = result;
 }
 
 template <typename S, bool kMax>
