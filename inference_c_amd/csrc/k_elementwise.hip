@@ -115,10 +115,12 @@ __global__ __launch_bounds__(kBlock) void map_vec_kernel(const S *__restrict__ a
                                                          S *__restrict__ y, size_t nvec,
                                                          size_t n, Op op) {
     constexpr int E = Vec16<S>::N;
-    const size_t stride = (size_t)gridDim.x * kBlock;
-    for (size_t first = (size_t)blockIdx.x * kBlock; first < nvec; first += stride) {
-        const size_t i = first + threadIdx.x;
-        if (i >= nvec) break;
+    // One-shot grid (the host covers nvec with one vector per lane): no
+    // grid-stride loop, whose stride -- the grid size, a hidden argument --
+    // was one more scalar-load round trip before the first vector load.
+    const size_t first = (size_t)blockIdx.x * kBlock;
+    const size_t i = first + threadIdx.x;
+    if (i < nvec) {
         const Vec16<S> va = load16_stream(a + i * E);
         Vec16<S> vb{};
         if constexpr (kArity == 2) vb = load16_stream(b + i * E);
@@ -162,6 +164,8 @@ hipError_t launch_map(const S *a, const S *b, S *y, size_t n, hipStream_t s) {
     constexpr int E = Vec16<S>::N;
     if (aligned16(a) && aligned16(b) && aligned16(y)) {
         const size_t nvec = n / E;
+        // map_vec_kernel covers nvec in one pass of the grid
+        if (nvec > size_t{0x7fffffff} * kBlock) return hipErrorInvalidValue;
         const unsigned grid = grid_for(nvec > 0 ? nvec : 1, (size_t)kBlock);
         if (write_through_for(n * sizeof(S)))
             hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, true>), dim3(grid), dim3(kBlock),
