@@ -221,21 +221,21 @@ __global__ __launch_bounds__(kBlock) void bias_vec_kernel(const S *__restrict__ 
                                                           S *__restrict__ y, uint32_t nvec,
                                                           FastDiv per_row) {
     constexpr int E = Vec16<S>::N;
-    const size_t stride = (size_t)gridDim.x * kBlock;
-    for (size_t first = (size_t)blockIdx.x * kBlock; first < nvec; first += stride) {
-        if (first + threadIdx.x >= nvec) break;
-        const uint32_t i = (uint32_t)(first + threadIdx.x);
-        const uint32_t row = fast_div(i, per_row);
-        const uint32_t col = i - row * per_row.divisor;
-        const Vec16<S> vx = load16_stream(x + (size_t)i * E);
-        const Vec16<S> vb = load16(bias + (size_t)col * E);
-        Vec16<S> out;
+    // one-shot grid (nvec < 2^32 vectors, one per lane): no grid-stride loop
+    // and so no round trip for the grid size before the loads
+    const size_t first = (size_t)blockIdx.x * kBlock;
+    if (first + threadIdx.x >= nvec) return;
+    const uint32_t i = (uint32_t)(first + threadIdx.x);
+    const uint32_t row = fast_div(i, per_row);
+    const uint32_t col = i - row * per_row.divisor;
+    const Vec16<S> vx = load16_stream(x + (size_t)i * E);
+    const Vec16<S> vb = load16(bias + (size_t)col * E);
+    Vec16<S> out;
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-            out.v[e] = Elem<S>::store(bias_value<S, kGelu>(Elem<S>::load(vx.v[e]),
-                                                           Elem<S>::load(vb.v[e])));
-        store_block_vec<kThrough>(y, first * E, out);
-    }
+    for (int e = 0; e < E; ++e)
+        out.v[e] = Elem<S>::store(bias_value<S, kGelu>(Elem<S>::load(vx.v[e]),
+                                                       Elem<S>::load(vb.v[e])));
+    store_block_vec<kThrough>(y, first * E, out);
 }
 
 template <typename S, bool kGelu>
