@@ -120,12 +120,12 @@ template <typename S, int kChunks, int kIt>
 __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S *__restrict__ k,
                                                             uint32_t seq, uint32_t qh,
                                                             uint32_t kh, uint32_t ppb,
-                                                            uint64_t offset, RopeDenoms denom) {
+                                                            FastDiv per_pos_div, uint64_t offset,
+                                                            RopeDenoms denom) {
     constexpr int E = Vec16<S>::N;
     constexpr uint32_t half = kChunks * E;
     extern __shared__ float2 rot[];  // ppb * half rotations
-    const uint32_t heads = qh + kh;
-    const uint32_t per_pos = heads * kChunks;
+    const uint32_t per_pos = per_pos_div.divisor;   // (qh + kh) * kChunks
     const uint32_t p0 = blockIdx.x * ppb;
     const uint32_t npos = min(ppb, seq - p0);
     const uint32_t items = npos * per_pos;
@@ -146,7 +146,9 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         const uint32_t raw = it0 + (u * (kBlock / kWave) + wave) * 32 + (lane & 31);
         ok[u] = raw < items;
         const uint32_t item = ok[u] ? raw : 0u;
-        const uint32_t pp = item / per_pos;
+        // multiply-high division: a 32-bit divide by the run-time per_pos was
+        // ~40 instructions in front of each of the lane's loads
+        const uint32_t pp = fast_div(item, per_pos_div);
         const uint32_t rest = item - pp * per_pos;
         const uint32_t row = rest / kChunks;
         const uint32_t c = rest - row * kChunks;
@@ -261,11 +263,12 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
         const size_t pairs_needed = (ppb * per_pos + kPairItems - 1) / kPairItems;
         const int it = pairs_needed <= 1 ? 1 : pairs_needed <= 2 ? 2 : pairs_needed <= 4 ? 4 : 8;
         const size_t splits = (ppb * per_pos + (size_t)it * kPairItems - 1) / ((size_t)it * kPairItems);
+        const FastDiv per_pos_div = make_fast_div((uint32_t)per_pos);
         const dim3 grid((unsigned)((seq + ppb - 1) / ppb), (unsigned)splits), block(kBlock);
         const size_t lds = ppb * half * sizeof(float2);
 #define ICSDK_ROPE(CH, IT)                                                                      \
     hipLaunchKernelGGL((rope_fused_kernel<S, CH, IT>), grid, block, lds, s, q, k, a, b, c, d,    \
-                       (uint64_t)offset, denom)
+                       per_pos_div, (uint64_t)offset, denom)
 #define ICSDK_ROPE_IT(CH)                                                                       \
     do {                                                                                        \
         if (it == 1) ICSDK_ROPE(CH, 1);                                                         \
