@@ -35,6 +35,18 @@ typedef enum {
     TENSOR_DTYPE_F64        /* 15 */
 } TensorDType;
 
+/* One tensor's metadata in a safetensors file or store (reference
+ * include/safetensors.h:30-37, layout kept: tensor_buffer_load reads dtype,
+ * rank, shape and byte_length from the record the store returns). */
+typedef struct {
+    const char *name;
+    TensorDType dtype;
+    size_t rank;
+    const uint64_t *shape;
+    uint64_t data_offset;
+    uint64_t byte_length;
+} SafeTensorInfo;
+
 /* Replaces src/common/safetensors.c's tensor_dtype_name / tensor_dtype_size
  * (declared at include/safetensors.h:41-42 of the reference). Unknown dtypes
  * have size 0 and name "UNKNOWN". */

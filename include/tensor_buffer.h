@@ -36,14 +36,16 @@ int tensor_buffer_create(TensorDType dtype, const uint64_t *shape, size_t rank,
 int tensor_buffer_create_device(TensorDType dtype, const uint64_t *shape,
                                 size_t rank, TensorBuffer **result,
                                 char *error, size_t error_capacity);
-/* reference :27-30. Workspace arenas are not part of this library: the call
-   reports that no workspace allocator is linked. */
+/* reference :27-30. The host data comes from the program's workspace arena
+   (the reference's tensor_workspace.c, reached through a weak reference);
+   without that code linked the call fails with a message. */
 int tensor_buffer_create_in_workspace(TensorDType dtype, const uint64_t *shape,
                                       size_t rank, TensorWorkspace *workspace,
                                       TensorBuffer **result, char *error,
                                       size_t error_capacity);
-/* reference :31-33. Weight stores are not part of this library: the call
-   reports that no tensor store is linked. */
+/* reference :31-33. Reads through the program's tensor store (the
+   reference's tensor_store.c, reached through weak references); without that
+   code linked the call fails with a message. */
 int tensor_buffer_load(const TensorStore *store, const char *tensor_name,
                        TensorBuffer **result, char *error,
                        size_t error_capacity);

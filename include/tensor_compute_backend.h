@@ -13,9 +13,12 @@
  *     in the reference test for NULL before calling.
  *
  * The HIP backend ("hip") fills the elementwise, broadcast, normalisation,
- * RoPE and argmax slots. GEMM-based slots (linear*, mlp*, qkv*, vision_*,
- * rms_norm_linear_f32, quantized linears) are contractions outside this
- * library and stay NULL.
+ * RoPE, argmax and embedding slots, and the GEMM-based linear*,
+ * linear*_device, linear_q8_0_f16 / linear_q4_0_f16 (+ _device),
+ * rms_norm_linear_f32, mlp_f16 and qkv_f16 slots (hipBLASLt GEMMs and the
+ * library's quantized GEMV/MFMA kernels; host-pointer weights stay on the
+ * device per host address until release_cache). The whole-layer slots
+ * (vision_layer_*, vision_sequence_*, mlp_f32) stay NULL.
  */
 #ifndef TENSOR_COMPUTE_BACKEND_H
 #define TENSOR_COMPUTE_BACKEND_H

@@ -12,9 +12,17 @@
  *     call returns when the host output has been written.
  * All operands of one call must share one storage kind.
  *
- * matmul / linear / embedding are GEMM or gather work that this library does
- * not provide: those entry points exist for link compatibility and fail with
- * a message naming the operation.
+ * matmul and linear also run on the GPU (hipBLASLt, f32 or f16 with f32
+ * accumulation; the linear's bias is added inside the GEMM before its one
+ * rounding). Device-storage linears go through the compute table returned by
+ * tensor_compute_preferred_backend(), as the reference does, so a
+ * TENSOR_BACKEND naming another backend makes them fail. The embedding
+ * lookups check every index before any row is written (host indices on the
+ * host; device indices by a one-block kernel whose verdict the call waits
+ * for), then gather the rows on the GPU.
+ *
+ * Without a HIP device every compute entry point fails with a message
+ * beginning "HIP device unavailable"; there is no CPU arithmetic path.
  */
 #ifndef TENSOR_OPS_H
 #define TENSOR_OPS_H

@@ -6,11 +6,19 @@
 // byte for empty tensors), device storage allocated only for non-empty
 // tensors, data() NULL for device tensors, range-checked upload / download /
 // device copy. tensor_buffer_convert runs on the GPU (ops.cpp).
+//
+// Workspace arenas and weight stores are the program's, not this library's:
+// tensor_buffer_create_in_workspace and tensor_buffer_load call the
+// reference's tensor_workspace_allocate / tensor_store_find /
+// tensor_store_read_raw through weak references. A program that holds a
+// TensorWorkspace or TensorStore has linked the code that made it, so the
+// references resolve; otherwise they stay null and the call reports it.
 #include "sdk.hpp"
 
 #include "tensor_buffer.h"
 #include "tensor_device.h"
 #include "tensor_f16.h"
+#include "tensor_store.h"
 
 #include <cstdint>
 #include <cstdlib>
@@ -25,7 +33,19 @@ struct TensorBuffer {
     void *data;                       // host storage
     TensorDeviceBuffer *device;       // device storage (NULL when empty)
     TensorBufferStorage storage;
+    bool owns_data;                   // false for workspace-backed host data
 };
+
+// reference include/tensor_workspace.h:17-19 (defined by tensor_workspace.c)
+extern "C" void *tensor_workspace_allocate(TensorWorkspace *workspace, size_t size,
+                                           size_t alignment, char *error,
+                                           size_t error_capacity) __attribute__((weak));
+extern "C" const SafeTensorInfo *tensor_store_find(const TensorStore *store,
+                                                   const char *tensor_name)
+    __attribute__((weak));
+extern "C" int tensor_store_read_raw(const TensorStore *store, const char *tensor_name,
+                                     void *destination, size_t capacity, char *error,
+                                     size_t error_capacity) __attribute__((weak));
 
 using icsdk::set_error;
 
@@ -33,8 +53,11 @@ namespace {
 
 constexpr size_t kMaxRank = 16;
 
+// workspace: host storage comes from the arena (reference
+// tensor_buffer.c:183-186, alignment _Alignof(max_align_t)), not the heap.
 int create(TensorDType dtype, const uint64_t *shape, size_t rank, bool host,
-           TensorBuffer **result, char *error, size_t capacity) {
+           TensorWorkspace *workspace, TensorBuffer **result, char *error,
+           size_t capacity) {
     if (result != nullptr) *result = nullptr;
     const size_t element_size = tensor_dtype_size(dtype);
     if (result == nullptr || element_size == 0 || rank > kMaxRank ||
@@ -75,7 +98,11 @@ int create(TensorDType dtype, const uint64_t *shape, size_t rank, bool host,
     buffer->byte_length = bytes;
     buffer->storage = host ? TENSOR_BUFFER_STORAGE_HOST : TENSOR_BUFFER_STORAGE_DEVICE;
     if (host) {
-        buffer->data = std::calloc(bytes == 0 ? 1 : bytes, 1);
+        buffer->data = workspace == nullptr
+                           ? std::calloc(bytes == 0 ? 1 : bytes, 1)
+                           : tensor_workspace_allocate(workspace, bytes, alignof(max_align_t),
+                                                       error, capacity);
+        buffer->owns_data = workspace == nullptr;
         if (buffer->data == nullptr) {
             std::free(buffer->shape);
             std::free(buffer);
@@ -181,7 +208,7 @@ float tensor_bf16_to_f32(uint16_t value) { return float_of((uint32_t)value << 16
 
 int tensor_buffer_create(TensorDType dtype, const uint64_t *shape, size_t rank,
                          TensorBuffer **result, char *error, size_t error_capacity) {
-    return create(dtype, shape, rank, true, result, error, error_capacity);
+    return create(dtype, shape, rank, true, nullptr, result, error, error_capacity);
 }
 
 int tensor_buffer_create_device(TensorDType dtype, const uint64_t *shape, size_t rank,
@@ -191,31 +218,61 @@ int tensor_buffer_create_device(TensorDType dtype, const uint64_t *shape, size_t
         set_error(error, error_capacity, "device tensor result pointer is required");
         return 0;
     }
-    return create(dtype, shape, rank, false, result, error, error_capacity);
+    return create(dtype, shape, rank, false, nullptr, result, error, error_capacity);
 }
 
+// reference src/common/tensor_buffer.c:235-246
 int tensor_buffer_create_in_workspace(TensorDType dtype, const uint64_t *shape, size_t rank,
                                       TensorWorkspace *workspace, TensorBuffer **result,
                                       char *error, size_t error_capacity) {
-    (void)dtype; (void)shape; (void)rank;
-    if (result != nullptr) *result = nullptr;
-    set_error(error, error_capacity,
-              workspace == nullptr ? "workspace-backed tensor requires a workspace"
-                                   : "workspace arenas are not part of the HIP tensor-ops library");
-    return 0;
+    if (workspace == nullptr) {
+        if (result != nullptr) *result = nullptr;
+        set_error(error, error_capacity, "workspace-backed tensor requires a workspace");
+        return 0;
+    }
+    if (tensor_workspace_allocate == nullptr) {
+        if (result != nullptr) *result = nullptr;
+        set_error(error, error_capacity,
+                  "workspace-backed tensor requires tensor_workspace.c linked into the program");
+        return 0;
+    }
+    return create(dtype, shape, rank, true, workspace, result, error, error_capacity);
 }
 
+// reference src/common/tensor_buffer.c:248-271: a host tensor of the stored
+// dtype and shape, filled with the stored bytes.
 int tensor_buffer_load(const TensorStore *store, const char *tensor_name,
                        TensorBuffer **result, char *error, size_t error_capacity) {
-    (void)store; (void)tensor_name;
     if (result != nullptr) *result = nullptr;
-    set_error(error, error_capacity, "tensor stores are not part of the HIP tensor-ops library");
-    return 0;
+    if (tensor_store_find == nullptr || tensor_store_read_raw == nullptr) {
+        set_error(error, error_capacity,
+                  "tensor_buffer_load requires tensor_store.c linked into the program");
+        return 0;
+    }
+    const SafeTensorInfo *info = tensor_store_find(store, tensor_name);
+    if (info == nullptr || result == nullptr) {
+        set_error(error, error_capacity, "tensor metadata was not found");
+        return 0;
+    }
+    TensorBuffer *buffer = nullptr;
+    if (!tensor_buffer_create(info->dtype, info->shape, info->rank, &buffer, error,
+                              error_capacity))
+        return 0;
+    if (buffer->byte_length != info->byte_length ||
+        !tensor_store_read_raw(store, tensor_name, buffer->data, buffer->byte_length, error,
+                               error_capacity)) {
+        tensor_buffer_free(buffer);
+        if (error != nullptr && error_capacity > 0 && error[0] == '\0')
+            set_error(error, error_capacity, "tensor metadata byte length mismatch");
+        return 0;
+    }
+    *result = buffer;
+    return 1;
 }
 
 void tensor_buffer_free(TensorBuffer *buffer) {
     if (buffer == nullptr) return;
-    std::free(buffer->data);
+    if (buffer->owns_data) std::free(buffer->data);
     tensor_device_buffer_free(buffer->device);
     std::free(buffer->shape);
     std::free(buffer);

@@ -294,13 +294,19 @@ class Sdk:
         return self.lib.tensor_device_hip_stream() or 0
 
 
+# Headers whose functions the calling program defines (the reference's
+# tensor_store.c); the library only references them weakly.
+PROGRAM_HEADERS = ("tensor_store.h",)
+
+
 def declared_functions(include_dir: str = INCLUDE_DIR) -> list[str]:
-    """Names of every function declared in include/*.h."""
+    """Names of every function the library exports, as declared in include/*.h
+    (all headers but PROGRAM_HEADERS)."""
     import re
     names = []
     pattern = re.compile(r"^[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", re.M)
     for fname in sorted(os.listdir(include_dir)):
-        if not fname.endswith(".h"):
+        if not fname.endswith(".h") or fname in PROGRAM_HEADERS:
             continue
         text = open(os.path.join(include_dir, fname)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)

@@ -129,11 +129,25 @@ def test_host_tensor_buffer_contract(lib):
         sdk.tensor("f32", (1 << 40, 1 << 40), device=False)
 
 
-def test_tensor_store_entry_points_fail_with_a_message(lib):
+def test_store_and_workspace_entry_points_without_that_code_linked(lib):
+    """In a process without the reference's tensor_store.c / tensor_workspace.c
+    (this Python process) the weak references stay null and both calls fail
+    with a message instead of jumping through a null pointer. With that code
+    linked, the reference's own test_tensor_store / test_tensor_workspace /
+    test_tensor_prefetch exercise them (test_dropin_reference.py)."""
     err = ctypes.create_string_buffer(256)
     res = ctypes.c_void_p(1)
     assert not lib.tensor_buffer_load(None, b"w", ctypes.byref(res), err, 256)
-    assert res.value is None and b"tensor stores are not part of" in err.value
+    assert res.value is None
+    assert err.value == b"tensor_buffer_load requires tensor_store.c linked into the program"
+    res = ctypes.c_void_p(1)
+    shape = (ctypes.c_uint64 * 1)(4)
+    assert not lib.tensor_buffer_create_in_workspace(14, shape, 1, None, ctypes.byref(res), err, 256)
+    assert res.value is None and err.value == b"workspace-backed tensor requires a workspace"
+    assert not lib.tensor_buffer_create_in_workspace(14, shape, 1, ctypes.c_void_p(8),
+                                                     ctypes.byref(res), err, 256)
+    assert res.value is None
+    assert err.value == b"workspace-backed tensor requires tensor_workspace.c linked into the program"
 
 
 def test_linear_and_matmul_validation_matches_reference(lib, ref, orc):
