@@ -164,6 +164,21 @@ int tensor_residual_rms_norm_f16(const TensorBuffer *input,
 int tensor_sum_max_f32(const TensorBuffer *input, TensorBuffer *sum_output,
                        TensorBuffer *max_output, char *error,
                        size_t error_capacity);
+/* tensor_sum_max_f32 without any allocation. No counterpart in the
+   reference: it is for callers that cannot allocate device memory (code
+   under HIP graph capture, serving loops that forbid hipMalloc). Same
+   validation, kernels and results as tensor_sum_max_f32; every operand must
+   be a device tensor (host operands are refused, since staging them would
+   allocate). The pass-1 partials live in a 128 KiB device array of the
+   library, one per GPU, held until the process ends; it covers every input
+   size (the pass-1 grid is capped), and a launch whose partials would not fit
+   is refused with a message. Pass 1 writes every partial pass 2 reads, so
+   the array keeps the last call's contents harmlessly. Calls are ordered on
+   the library's one stream; any other use of the array that overlaps a call
+   on the same GPU races with it. */
+int tensor_sum_max_f32_no_alloc(const TensorBuffer *input, TensorBuffer *sum_output,
+                                TensorBuffer *max_output, char *error,
+                                size_t error_capacity);
 /* Index (U32 [1] output) of the first maximum, with the reference's scan
    semantics (tensor_compute_cuda.cu:386-397): NaN elements never win, and if
    element 0 is NaN the result is 0. At most 2^32-1 elements. */

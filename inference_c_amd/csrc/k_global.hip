@@ -14,6 +14,8 @@
 #include "kern_common.hpp"
 #include "kernels.hpp"
 
+#include <mutex>
+
 namespace icsdk {
 namespace {
 
@@ -252,8 +254,56 @@ inline int pass1_grid(size_t work) {
 }
 
 }  // namespace
+}  // namespace icsdk
 
+// Partials of the allocation-free sum+max (tensor_sum_max_f32_no_alloc): one
+// Partial per pass-1 block, and the pass-1 grid never exceeds kMaxPartials
+// blocks (past that the blocks stride over chunks), so 128 KiB covers every
+// input size. Each device the library runs on holds its own copy until the
+// process ends. Host code never passes this name to a kernel: its device
+// address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char
+    scratch[sizeof(icsdk::Partial) * icsdk::kMaxPartials];
+
+namespace icsdk {
 namespace k {
+
+size_t no_alloc_scratch_bytes() { return sizeof(scratch); }
+
+hipError_t no_alloc_scratch(void **ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex lookup;
+    static void *address[kMaxDevices] = {};
+    *ptr = nullptr;
+    int device = -1;
+    hipError_t status = hipGetDevice(&device);
+    if (status != hipSuccess) return status;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(lookup);
+    if (address[device] == nullptr) {
+        void *found = nullptr;
+        status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+        if (status != hipSuccess) return status;
+        address[device] = found;
+    }
+    *ptr = address[device];
+    return hipSuccess;
+}
+
+size_t sum_max_partials_bytes(size_t n) {
+    const size_t chunks = (n / 4 + kChunk - 1) / kChunk;
+    const size_t grid = chunks < 1 ? 1 : (chunks > (size_t)kMaxPartials ? kMaxPartials : chunks);
+    return grid * sizeof(Partial);
+}
+
+hipError_t sum_max_f32_no_alloc(const float *x, size_t n, double *sum_out, float *max_out,
+                                void *scratch_ptr, size_t scratch_bytes, hipStream_t s) {
+    if (n == 0 || ((uintptr_t)x & 15u) != 0 || scratch_ptr == nullptr ||
+        sum_max_partials_bytes(n) > scratch_bytes)
+        return hipErrorInvalidValue;
+    return sum_max_f32(x, n, sum_out, max_out, scratch_ptr, s);
+}
+
 
 size_t grid_reduce_scratch_bytes() {
     return sizeof(Partial) * (kMaxPartials > kPartials ? kMaxPartials : kPartials);
@@ -264,9 +314,7 @@ hipError_t sum_max_f32(const float *x, size_t n, double *sum_out, float *max_out
     if (n == 0) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15u) != 0) return hipErrorInvalidValue;
     const size_t nvec = n / 4;
-    size_t chunks = (nvec + kChunk - 1) / kChunk;
-    if (chunks < 1) chunks = 1;
-    const int grid = chunks > (size_t)kMaxPartials ? kMaxPartials : (int)chunks;
+    const int grid = (int)(sum_max_partials_bytes(n) / sizeof(Partial));
     auto *p = static_cast<Partial *>(partials);
     hipLaunchKernelGGL(sum_max_pass1, dim3(grid), dim3(kBlock), 0, s, x, nvec, n, p);
     hipLaunchKernelGGL(sum_max_pass2, dim3(1), dim3(kFoldBlock), 0, s, p, grid, sum_out,

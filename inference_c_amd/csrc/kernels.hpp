@@ -64,6 +64,18 @@ hipError_t row_max_f16(const uint16_t *x, float *y, size_t rows, size_t width,
 size_t grid_reduce_scratch_bytes();
 hipError_t sum_max_f32(const float *x, size_t n, double *sum_out, float *max_out,
                        void *partials, hipStream_t s);
+// Bytes of partials sum_max_f32 writes for n elements (at most
+// grid_reduce_scratch_bytes()).
+size_t sum_max_partials_bytes(size_t n);
+// The allocation-free variant's partials: a file-scope device array of
+// no_alloc_scratch_bytes() bytes in k_global.hip. no_alloc_scratch() returns
+// its address on the current device (looked up once per device);
+// sum_max_f32_no_alloc() runs sum_max_f32 with it and refuses a launch whose
+// partials would not fit in scratch_bytes.
+size_t no_alloc_scratch_bytes();
+hipError_t no_alloc_scratch(void **ptr);
+hipError_t sum_max_f32_no_alloc(const float *x, size_t n, double *sum_out, float *max_out,
+                                void *scratch_ptr, size_t scratch_bytes, hipStream_t s);
 hipError_t argmax_f32(const float *x, size_t n, uint32_t *index_out, void *partials,
                       hipStream_t s);
 hipError_t argmax_f16(const uint16_t *x, size_t n, uint32_t *index_out, void *partials,

@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 
 using namespace icsdk;
 
@@ -800,6 +801,65 @@ int tensor_sum_max_f32(Buf x, TensorBuffer *sum, TensorBuffer *max, char *error,
                                 as<float>(pm), partials, st.stream());
     }
     return st.finish(status) ? 1 : 0;
+}
+
+// tensor_sum_max_f32 for callers that cannot allocate (code under HIP graph
+// capture, serving loops that forbid hipMalloc). Same validation, kernels and
+// results; the operands must be device tensors (host operands would be staged
+// through allocated memory), and the pass-1 partials live in the library's
+// 128 KiB device array instead of the grid-reduction buffer. Nothing here
+// allocates: the array's address is looked up once per device
+// (hipGetSymbolAddress), launches go to the SDK stream. Pass 1 writes every
+// partial pass 2 reads, so the array needs no clearing between calls; calls
+// enqueued on one GPU from this library are ordered by the SDK stream and the
+// mutex below, and any other use of the array that overlaps them races.
+int tensor_sum_max_f32_no_alloc(Buf x, TensorBuffer *sum, TensorBuffer *max, char *error,
+                                size_t capacity) {
+    if (!is(x, TENSOR_DTYPE_F32) || tensor_buffer_element_count(x) == 0 ||
+        (sum == nullptr && max == nullptr) ||
+        (sum != nullptr && (!is(sum, TENSOR_DTYPE_F64) || tensor_buffer_element_count(sum) != 1)) ||
+        (max != nullptr && (!is(max, TENSOR_DTYPE_F32) || tensor_buffer_element_count(max) != 1))) {
+        set_error(error, capacity,
+                  "sum/max requires a non-empty F32 input, a one-element F64 sum output "
+                  "and/or a one-element F32 max output");
+        return 0;
+    }
+    for (Buf t : {x, static_cast<Buf>(sum), static_cast<Buf>(max)}) {
+        if (t != nullptr && tensor_buffer_storage(t) != TENSOR_BUFFER_STORAGE_DEVICE) {
+            set_error(error, capacity,
+                      "sum/max without allocation requires device-storage operands");
+            return 0;
+        }
+    }
+    const size_t n = tensor_buffer_element_count(x);
+    const size_t need = k::sum_max_partials_bytes(n);
+    if (need > k::no_alloc_scratch_bytes()) {
+        set_error(error, capacity,
+                  "sum/max without allocation needs %zu bytes of partials for %zu elements, "
+                  "more than its %zu-byte scratch",
+                  need, n, k::no_alloc_scratch_bytes());
+        return 0;
+    }
+    if (!sdk_ready(error, capacity)) return 0;
+    void *scratch = nullptr;
+    if (!hip_ok(k::no_alloc_scratch(&scratch), "sum/max scratch address (hipGetSymbolAddress)",
+                error, capacity))
+        return 0;
+    static std::mutex order;
+    hipError_t status;
+    {
+        std::lock_guard<std::mutex> lock(order);
+        status = k::sum_max_f32_no_alloc(
+            as<float>(tensor_buffer_device_handle_internal(x)), n,
+            sum == nullptr ? nullptr : as<double>(tensor_buffer_device_handle_internal(sum)),
+            max == nullptr ? nullptr : as<float>(tensor_buffer_device_handle_internal(max)),
+            scratch, k::no_alloc_scratch_bytes(), sdk_stream());
+    }
+    if (status != hipSuccess) {
+        set_error(error, capacity, "sum/max: kernel launch failed: %s", hipGetErrorString(status));
+        return 0;
+    }
+    return 1;
 }
 
 int tensor_argmax_f32(Buf x, TensorBuffer *index, char *error, size_t capacity) {

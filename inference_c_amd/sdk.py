@@ -52,7 +52,7 @@ OP_ARGTYPES = {
     "tensor_row_sum_f32": [_P, _P], "tensor_row_sum_f16": [_P, _P],
     "tensor_row_max_f32": [_P, _P], "tensor_row_max_f16": [_P, _P],
     "tensor_residual_rms_norm_f16": [_P, _P, _P, _F, _P, _P],
-    "tensor_sum_max_f32": [_P, _P, _P],
+    "tensor_sum_max_f32": [_P, _P, _P], "tensor_sum_max_f32_no_alloc": [_P, _P, _P],
     "tensor_argmax_f32": [_P, _P], "tensor_argmax_f16": [_P, _P],
     "tensor_rope_f32": [_P, _P, _Z, _Z, _Z, _D, _Z], "tensor_rope_f16": [_P, _P, _Z, _Z, _Z, _D, _Z],
     "tensor_fill_uniform": [_P, _U64, _U64, _F, _F], "tensor_fill_normal": [_P, _U64, _U64, _F, _F],
