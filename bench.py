@@ -1,21 +1,26 @@
 #!/usr/bin/env python3
 """Throughput of the HIP tensor-ops kernels on one MI355X.
 
-Step: one pass of the FP16 unary/fused elementwise
-workload -- SiLU and tanh-GELU on [8192, 8192] f16 N(0,1) and SwiGLU
-out = a * silu(b) on [4096, 16384] f16 N(0,1), seed 1 -- with every input
-already resident in HBM. `value` is the step's algorithmic bytes (each input
-read once, each output written once) over the wall time of K steps. The K
-launches of each kernel run back to back between HIP events on the SDK
-stream (the stream the kernels run on), which gives each kernel's average
-launch duration; the dominant kernel's achieved GB/s against the 8 TB/s HBM
-peak is `roofline`. Operands rotate over enough identical copies that no
-launch is served from the 256 MB last-level cache.
+Step (the largest single-GPU configuration): one
+pass of the decoder-layer non-GEMM chain at tokens 4096, hidden 2048,
+intermediate 8192 in f16 -- fused residual add + RMSNorm, RoPE on q and k
+[4096, 32, 64] (theta 1e4, positions 0..4095) and SwiGLU on [4096, 8192] --
+followed by the global sum + max over 2^30 f32 elements U[-1,1], every input
+resident in HBM. `value` is the step's algorithmic bytes (each input read
+once, each output written once) over the wall time of K steps. HIP events on
+the SDK stream (the stream the kernels run on) mark each step's start and the
+end of its chain, which gives the chain's and the global reduction's average
+durations; the dominant call, the global sum/max (4 GiB read), against the
+8 TB/s HBM peak is `roofline`. The 4 GiB read of every step evicts the
+chain's operands from the 256 MB last-level cache, so each step's chain
+starts from HBM.
 
-The other BASELINE configs are timed per kernel the same way and reported
-under "suite". The CPU baseline times the oracle (a single-threaded C
-restatement of the reference's portable path) on a bounded slice of the same
-workload.
+The other BASELINE configs (configs[1]'s SiLU/GELU/SwiGLU among them) are
+timed per kernel and reported under "suite". `cpu_baseline` times the
+reference's portable C path (oracle/_ref/libref.so, its own tensor_ops
+functions on host TensorBuffers) where the reference has the op, and the
+oracle's C restatement elsewhere, single-threaded on a stated sample of each
+config.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
 """
@@ -41,6 +46,14 @@ CFG2 = {
     "gelu_f16": (268_435_456, 67_108_864),
     "swiglu_f16": (402_653_184, 67_108_864),
 }
+# the chain's calls and the global reduction, in step order
+CFG5 = {
+    "cfg5_residual_rms_norm_f16": (67_112_960, 8_388_608),
+    "cfg5_rope_f16": (67_108_864, 16_777_216),
+    "cfg5_swiglu_f16": (201_326_592, 33_554_432),
+    "cfg5_global_sum_max_f32": (4_294_967_296, 1_073_741_824),
+}
+CFG5_CHAIN_ELEMENTS = 142_606_336  # the chain's element count
 
 
 class Hip:
@@ -94,44 +107,197 @@ def measured_traffic(kernel):
     return None
 
 
-def cpu_baseline(rows_fraction=4):
-    """Oracle (single thread) on the first 1/rows_fraction of each cfg2 tensor,
-    median of 5 after 1 warmup; reported in the metric's unit (GB/s of the
-    same algorithmic bytes)."""
+def cpu_baseline(suite_results=None, step_kernels=None, reps=5):
+    """One CPU figure per BASELINE config, single-threaded, each op on a
+    stated sample of its config (1 warmup, median of `reps` timed calls,
+    time.perf_counter = CLOCK_MONOTONIC), in the metric's unit: GB/s of the
+    same algorithmic bytes, elements/s, and the GPU/CPU ratio against the
+    GPU figure of this run. kind "reference": the reference's own tensor_ops
+    function (oracle/_ref/libref.so, built from its sources) on host
+    TensorBuffers, timed around that call alone. kind "port": the oracle's C
+    restatement (oracle/liboracle.so, -O3) of the reference code named in
+    `source`, for ops the reference computes only inside other code; "closed
+    form" for ops the reference lacks. The top-level value is configs[4]'s
+    step (the bench step): each op's time scaled from its sample to the full
+    shape, summed."""
     import numpy as np
-    from oracle import Oracle
-    orc = Oracle()
-    x = orc.normal((8192 // rows_fraction, 8192), 1, 0, 0.0, 1.0)
-    a = orc.normal((4096 // rows_fraction, 16384), 1, 1, 0.0, 1.0)
-    b = orc.normal((4096 // rows_fraction, 16384), 1, 2, 0.0, 1.0)
-    times = []
-    for rep in range(6):
-        t0 = time.perf_counter()
-        orc.silu(x)
-        orc.gelu(x)
-        orc.silu_multiply(b, a)
-        dt = time.perf_counter() - t0
-        if rep:
-            times.append(dt)
-    med = statistics.median(times)
-    step_bytes = sum(v[0] for v in CFG2.values()) / rows_fraction
-    del np
-    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle/liboracle.so (C restatement, -O3, 1 thread) on the first 1/"
-                       f"{rows_fraction} of the rows of each cfg2 tensor: SiLU+GELU "
-                       f"[{8192 // rows_fraction},8192], SwiGLU [{4096 // rows_fraction},16384]; "
-                       f"median of 5 after 1 warmup = {med:.3f} s"),
-            "cpu_model": _cpu_model(), "host_cores": os.cpu_count()}
+    from oracle import Oracle, load_reference
+    orc, ref = Oracle(), load_reference()
+    err = ctypes.create_string_buffer(256)
+    gpu = dict(suite_results or {})
+    gpu.update(step_kernels or {})   # the step's own figures where it has them
+    entries = []
+
+    def median_s(fn):
+        fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    def ref_op(name, ins, out, *scalars):
+        """Reference call on prepared host TensorBuffers: fn(*ins, *scalars,
+        out, error, capacity)."""
+        handles = [ref._make("f16" if a.dtype == np.float16 else "f32", a) for a in ins]
+        ho = ref._make("f16" if out.dtype == np.float16 else "f32", out)
+        fn = getattr(ref.lib, name)
+
+        def run():
+            assert fn(*handles, *scalars, ho, err, 256), err.value
+        return run, handles + [ho]
+
+    def record(cfg, op, kind, source, sample, run, sample_bytes, sample_elems, full_bytes,
+               gpu_key):
+        sec = median_s(run)
+        e = {"config": cfg, "op": op, "kind": kind, "source": source, "sample": sample,
+             "seconds": round(sec, 5), "gbps": round(sample_bytes / sec / 1e9, 4),
+             "elements_per_s": float(f"{sample_elems / sec:.4g}"),
+             "full_size_seconds_est": round(sec * full_bytes / sample_bytes, 3)}
+        g = gpu.get(gpu_key)
+        if g is not None and g.get("gbps"):
+            e["gpu_gbps"] = g["gbps"]
+            e["gpu_over_cpu"] = round(g["gbps"] / e["gbps"], 1)
+        entries.append(e)
+        return e
+
+    # cfg1: f32 [1024, 4096] U[-1,1] seed 0, full size
+    a = orc.uniform((1024, 4096), 0, 0, -1.0, 1.0)
+    b = orc.uniform((1024, 4096), 0, 1, -1.0, 1.0)
+    bias = orc.uniform((4096,), 0, 2, -1.0, 1.0)
+    full = "full size [1024,4096]"
+    record("cfg1", "add_f32", "port", "tensor_graph.c:453-459 (GRAPH_ADD loop)", full,
+           lambda: orc.add(a, b), 50_331_648, 4_194_304, 50_331_648, "cfg1_add_f32")
+    record("cfg1", "mul_f32", "closed form", "none in the reference", full,
+           lambda: orc.mul(a, b), 50_331_648, 4_194_304, 50_331_648, "cfg1_mul_f32")
+    record("cfg1", "bias_add_f32", "port", "tensor_compute_cuda.cu:338-359 (i % width)", full,
+           lambda: orc.bias_add(a, bias), 33_570_816, 4_194_304, 33_570_816,
+           "cfg1_bias_add_f32")
+    del a, b
+    # cfg2: f16 N(0,1) seed 1
+    x = orc.normal((512, 8192), 1, 0, 0.0, 1.0)
+    run, hs = ref_op("tensor_silu_f16", [x], np.zeros_like(x))
+    record("cfg2", "silu_f16", "reference", "tensor_ops.c:545-573 (tensor_silu_f16)",
+           "rows 0..511 of [8192,8192] (1/16)", run, 2 * x.nbytes, x.size, 268_435_456,
+           "cfg2_silu_f16")
+    for h in hs:
+        ref.lib.tensor_buffer_free(h)
+    xg = x[:256]
+    record("cfg2", "gelu_f16", "port", "vision_model.c:230-254 (tanh-GELU, +-5 clamps)",
+           "rows 0..255 of [8192,8192] (1/32)", lambda: orc.gelu(xg), 2 * xg.nbytes, xg.size,
+           268_435_456, "cfg2_gelu_f16")
+    ga = orc.normal((256, 16384), 1, 1, 0.0, 1.0)
+    gb = orc.normal((256, 16384), 1, 2, 0.0, 1.0)
+    record("cfg2", "swiglu_f16", "port", "text_model.c:876-884 (a * silu(b))",
+           "rows 0..255 of [4096,16384] (1/16)", lambda: orc.silu_multiply(gb, ga),
+           3 * ga.nbytes, ga.size, 402_653_184, "cfg2_swiglu_f16")
+    del x, xg, ga, gb
+    # cfg3: RMSNorm [16384, 2048], logits [32*2048, 2048] N(0,3), seed 3
+    x3 = orc.normal((2048, 2048), 3, 0, 0.0, 1.0)
+    w3 = orc.uniform((2048,), 3, 1, 0.5, 1.5, "f16")
+    run, hs = ref_op("tensor_rms_norm_f16", [x3, w3], np.zeros_like(x3), ctypes.c_float(1e-6))
+    record("cfg3", "rms_norm_f16", "reference", "tensor_ops.c:432-459 (tensor_rms_norm_f16)",
+           "rows 0..2047 of [16384,2048] (1/8)", run, 2 * x3.nbytes + w3.nbytes, x3.size,
+           134_221_824, "cfg3_rms_norm_f16")
+    for h in hs:
+        ref.lib.tensor_buffer_free(h)
+    lg = orc.normal((2048, 2048), 3, 2, 0.0, 3.0)
+    record("cfg3", "causal_softmax_f16", "port",
+           "attention.c:335-380 (the softmax inside tensor_sdpa_f32; no standalone entry point)",
+           "head 0: rows 0..2047 of [65536,2048] (1/32)", lambda: orc.softmax(lg, True),
+           2 * lg.nbytes, lg.size, 536_870_912, "cfg3_causal_softmax_f16")
+    record("cfg3", "row_sum_f16", "closed form", "none in the reference",
+           "rows 0..2047 of [65536,2048] (1/32)", lambda: orc.row_sum(lg),
+           lg.nbytes + 2048 * 4, lg.size, 268_697_600, "cfg3_row_sum_f16")
+    record("cfg3", "row_max_f16", "closed form", "none in the reference",
+           "rows 0..2047 of [65536,2048] (1/32)", lambda: orc.row_max(lg),
+           lg.nbytes + 2048 * 4, lg.size, 268_697_600, "cfg3_row_max_f16")
+    del x3, lg
+    # cfg4: x [B,S,H,D] read as (0,2,1,3), + A[1,H,1,D], * M[B,1,S,1]; one batch of 16
+    S4, H4, D4 = 1024, 32, 64
+    x4 = orc.normal((1, S4, H4, D4), 4, 0, 0.0, 1.0)
+    a4 = orc.uniform((1, H4, 1, D4), 4, 1, -1.0, 1.0, "f16")
+    m4 = orc.uniform((1, 1, S4, 1), 4, 2, -1.0, 1.0, "f16")
+    record("cfg4", "permuted_broadcast_f16", "closed form", "none in the reference",
+           "batch 0 of 16 (1/16)",
+           lambda: orc.view_add_mul(x4, (1, H4, S4, D4), (S4 * H4 * D4, D4, H4 * D4, 1), 0,
+                                    a4, m4),
+           2 * x4.nbytes + a4.nbytes + m4.nbytes, x4.size, 134_254_592,
+           "cfg4_permuted_broadcast_f16")
+    del x4
+    # cfg5: the chain on tokens 0..511 (1/8), the global reduction on 2^24 elements (1/64)
+    T5 = 512
+    x5 = orc.normal((T5, 2048), 5, 0, 0.0, 1.0)
+    r5 = orc.normal((T5, 2048), 5, 1, 0.0, 1.0)
+    w5 = orc.normal((2048,), 5, 9, 0.0, 1.0)
+    hx, hr, hw = ref._make("f16", x5), ref._make("f16", r5), ref._make("f16", w5)
+    hh, hn = ref._make("f16", np.zeros_like(x5)), ref._make("f16", np.zeros_like(x5))
+
+    def residual_norm():
+        assert ref.lib.tensor_residual_add_f16(hx, hr, hh, err, 256), err.value
+        assert ref.lib.tensor_rms_norm_f16(hh, hw, ctypes.c_float(1e-6), hn, err, 256), err.value
+    sample5 = "tokens 0..511 of 4096 (1/8)"
+    step = [record("cfg5", "residual_add + rms_norm_f16", "reference",
+                   "tensor_ops.c:575-622 then :432-459 (two calls; bytes counted as the fused "
+                   "kernel's)", sample5, residual_norm, 4 * x5.nbytes + w5.nbytes, x5.size,
+                   CFG5["cfg5_residual_rms_norm_f16"][0], "cfg5_residual_rms_norm_f16")]
+    for h in (hx, hr, hw, hh, hn):
+        ref.lib.tensor_buffer_free(h)
+    q5 = orc.normal((T5, 32, 64), 5, 2, 0.0, 1.0)
+    k5 = orc.normal((T5, 32, 64), 5, 3, 0.0, 1.0)
+    step.append(record("cfg5", "rope_f16", "port", "text_model.c:463-497 (double pow angle)",
+                       sample5, lambda: orc.rope(q5, k5, 32, 32, 64, 10000.0),
+                       2 * (q5.nbytes + k5.nbytes), 2 * q5.size, CFG5["cfg5_rope_f16"][0],
+                       "cfg5_rope_f16"))
+    g5 = orc.normal((T5, 8192), 5, 4, 0.0, 1.0)
+    u5 = orc.normal((T5, 8192), 5, 5, 0.0, 1.0)
+    step.append(record("cfg5", "swiglu_f16", "port", "text_model.c:876-884", sample5,
+                       lambda: orc.silu_multiply(g5, u5), 3 * g5.nbytes, g5.size,
+                       CFG5["cfg5_swiglu_f16"][0], "cfg5_swiglu_f16"))
+    big = orc.uniform((1 << 24,), 0, 0, -1.0, 1.0)
+    step.append(record("cfg5", "global_sum_max_f32", "closed form",
+                       "none in the reference (nearest: argmax scan, tensor_compute_cuda.cu:"
+                       "386-397)", "elements 0..2^24-1 of 2^30 (1/64)",
+                       lambda: orc.sum_max(big), big.nbytes, big.size,
+                       CFG5["cfg5_global_sum_max_f32"][0], "cfg5_global_sum_max_f32"))
+    del q5, k5, g5, u5, big
+    step_seconds = sum(e["full_size_seconds_est"] for e in step)
+    step_bytes = sum(v[0] for v in CFG5.values())
+    return {"value": round(step_bytes / step_seconds / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": ("configs[4] step (the bench step) on one host thread: residual add + "
+                       "RMSNorm through the reference's own tensor_ops.c (libref.so), RoPE and "
+                       "SwiGLU through the oracle's restatement of text_model.c, global sum+max "
+                       "closed form; chain on tokens 0..511 of 4096, global on 2^24 of 2^30 "
+                       "elements; each op's median time scaled to its full shape, summed = "
+                       f"{step_seconds:.3f} s per step"),
+            "step_seconds_est": round(step_seconds, 3),
+            "per_config": entries, "cpu_model": _cpu_model(), **_cpu_counts()}
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with family / model / stepping
+    (some virtual machines report a shortened model name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, value = (p.strip() for p in line.split(":", 1))
+                info.setdefault(key, value)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{info.get('model name', 'unknown')} (vendor {info.get('vendor_id', '?')}, family "
+            f"{info.get('cpu family', '?')}, model {info.get('model', '?')}, stepping "
+            f"{info.get('stepping', '?')})")
+
+
+def _cpu_counts():
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"nproc": usable, "host_cpus": os.cpu_count()}
 
 
 # ---- per-config kernel suite ------------------------------------------------
@@ -139,7 +305,7 @@ def _cpu_model():
 ROTATE_BYTES = 600 << 20  # traffic between two uses of the same buffers (> 256 MB MALL)
 
 
-def suite(sdk, hip, stream, reps=20, rounds=3):
+def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
     """Each BASELINE config's kernels: `reps` back-to-back launches between
     two events on the SDK stream, average per launch; the best of `rounds`
     such batches is reported with all of them. Every launch rotates to the
@@ -150,10 +316,13 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     (`copy_same_bytes_us`, `pct_of_copy`): below ~256 MB a single launch's
     fixed cost (launch, first-load latency, drain) keeps even a copy well
     under the 8 TB/s peak, and this is the ceiling a kernel of that size can
-    be held to."""
+    be held to. `only`: a set of result names to time (all when None)."""
     import numpy as np
     from inference_c_amd import TensorView
     results = {}
+
+    def wanted(name):
+        return only is None or name in only
     T = sdk.tensor
 
     def filled(dtype, shape, kind, seed, stream_id, a, b):
@@ -195,6 +364,8 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
         return copy_floor[alg_bytes]
 
     def measure(name, make_set, run, alg_bytes, elements):
+        if not wanted(name):
+            return
         batches, copies = timed(make_set, run, alg_bytes)
         best = min(batches)
         floor = copy_us(alg_bytes)
@@ -206,6 +377,15 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
                          "bytes": alg_bytes, "buffer_sets": copies,
                          "copy_same_bytes_us": round(floor * 1e3, 2),
                          "pct_of_copy": round(100 * floor / best, 1)}
+        traffic = measured_traffic(name)
+        if traffic is not None:
+            # HBM bytes the kernel actually moved (counter runs): the rate on
+            # real traffic, beside the algorithmic figure above
+            results[name].update({"traffic_bytes": traffic,
+                                  "traffic_over_algorithmic": round(traffic / alg_bytes, 4),
+                                  "gbps_traffic": round(traffic / (best * 1e-3) / 1e9, 1),
+                                  "pct_peak_traffic": round(100 * traffic / (best * 1e-3) / 1e9
+                                                            / PEAK_GBPS, 1)})
 
     # cfg1: f32 add / mul / row-bias add [1024, 4096], U[-1,1], seed 0
     def cfg1():
@@ -285,7 +465,8 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     # a [32000, 2048] f16 table; device storage, so each call also runs the
     # one-block index check and waits for its verdict before gathering
     vocab, width, tokens = 32000, 2048, 32768
-    emb_table = filled("f16", (vocab, width), "normal", 6, 0, 0.0, 1.0)
+    emb_table = filled("f16", (vocab, width), "normal", 6, 0, 0.0, 1.0) \
+        if wanted("embedding_lookup_f16") else None
     def gather_set():
         ids = T("i32", (tokens,))
         host_ids = ((np.arange(tokens, dtype=np.int64) * 2654435761) % vocab).astype(np.int32)
@@ -306,8 +487,12 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
         return raw
     for fmt, block in (("q8_0", 34), ("q4_0", 18)):
         out_f, in_f = 28672, 8192
+        row_counts = [r for r in ((1, 4, 16) if fmt == "q8_0" else (1,))
+                      if wanted(f"linear_{fmt}_f16_{r}x{in_f}_to_{out_f}")]
+        if not row_counts:
+            continue
         host_w = packed_weights(out_f, in_f, block)
-        for rows in ((1, 4, 16) if fmt == "q8_0" else (1,)):
+        for rows in row_counts:
             def quant_set(rows=rows, host_w=host_w):
                 return (T("u8", host_w.shape).upload(host_w),
                         filled("f16", (rows, in_f), "normal", 7, 3, 0.0, 1.0),
@@ -328,41 +513,47 @@ def suite(sdk, hip, stream, reps=20, rounds=3):
     rows_p = in_p = out_p = 4096
     p_flops = 2.0 * rows_p * in_p * out_p
     p_bytes = (rows_p * in_p + out_p * in_p + rows_p * out_p + out_p) * 2
-    batches, _ = timed(linear_set(rows_p, in_p, out_p), run_linear, p_bytes)
-    best = min(batches)
-    results["linear_f16_prefill_4096x4096_to_4096_bias"] = {
-        "avg_us": round(best * 1e3, 2), "batches_us": [round(t * 1e3, 2) for t in batches],
-        "tflops": round(p_flops / (best * 1e-3) / 1e12, 1),
-        "pct_peak_mfma": round(100 * p_flops / (best * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f16"], 1),
-        "peak_tflops": MFMA_PEAK_TFLOPS["f16"], "flops": p_flops, "bytes": p_bytes,
-        "library": "hipBLASLt (bias epilogue)"}
+    name_p = "linear_f16_prefill_4096x4096_to_4096_bias"
+    if wanted(name_p):
+        batches, _ = timed(linear_set(rows_p, in_p, out_p), run_linear, p_bytes)
+        best = min(batches)
+        results[name_p] = {
+            "avg_us": round(best * 1e3, 2), "batches_us": [round(t * 1e3, 2) for t in batches],
+            "tflops": round(p_flops / (best * 1e-3) / 1e12, 1),
+            "pct_peak_mfma": round(100 * p_flops / (best * 1e-3) / 1e12
+                                   / MFMA_PEAK_TFLOPS["f16"], 1),
+            "peak_tflops": MFMA_PEAK_TFLOPS["f16"], "flops": p_flops, "bytes": p_bytes,
+            "library": "hipBLASLt (bias epilogue)"}
     # host-pointer compute-table slot (PCIe included, never `value`): SwiGLU
     # on cfg2's [4096, 16384] f16 operands in pageable host memory, staged
     # through the pinned chunk pool; wall clock of the synchronous call
-    import ctypes as _ct
-    table = sdk.compute_table()
-    slot = _ct.CFUNCTYPE(_ct.c_int, _ct.c_void_p, _ct.c_void_p, _ct.c_void_p,
-                         _ct.c_size_t)(table.silu_multiply_f16)
-    n_host = 4096 * 16384
-    ha = np.random.default_rng(1).standard_normal(n_host).astype(np.float16)
-    hb = np.random.default_rng(2).standard_normal(n_host).astype(np.float16)
-    hy = np.empty_like(ha)
-    assert slot(ha.ctypes.data, hb.ctypes.data, hy.ctypes.data, n_host)
-    walls = []
-    for _ in range(5):
-        t0 = time.perf_counter()
+    if wanted("host_slot_swiglu_f16_pcie"):
+        import ctypes as _ct
+        table = sdk.compute_table()
+        slot = _ct.CFUNCTYPE(_ct.c_int, _ct.c_void_p, _ct.c_void_p, _ct.c_void_p,
+                             _ct.c_size_t)(table.silu_multiply_f16)
+        n_host = 4096 * 16384
+        ha = np.random.default_rng(1).standard_normal(n_host).astype(np.float16)
+        hb = np.random.default_rng(2).standard_normal(n_host).astype(np.float16)
+        hy = np.empty_like(ha)
         assert slot(ha.ctypes.data, hb.ctypes.data, hy.ctypes.data, n_host)
-        walls.append(time.perf_counter() - t0)
-    wall = statistics.median(walls)
-    results["host_slot_swiglu_f16_pcie"] = {
-        "wall_us": round(wall * 1e6, 1), "bytes": 3 * 2 * n_host,
-        "gbps_pcie_inclusive": round(3 * 2 * n_host / wall / 1e9, 2),
-        "note": "inputs and output in pageable host memory; median of 5 synchronous calls"}
-    del ha, hb, hy
+        walls = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            assert slot(ha.ctypes.data, hb.ctypes.data, hy.ctypes.data, n_host)
+            walls.append(time.perf_counter() - t0)
+        wall = statistics.median(walls)
+        results["host_slot_swiglu_f16_pcie"] = {
+            "wall_us": round(wall * 1e6, 1), "bytes": 3 * 2 * n_host,
+            "gbps_pcie_inclusive": round(3 * 2 * n_host / wall / 1e9, 2),
+            "note": "inputs and output in pageable host memory; median of 5 synchronous calls"}
+        del ha, hb, hy
     # attention (MFMA-bound, not HBM): scaled dot-product attention on device
     # buffers; flops = 4 * B * Hq * Lq * Lkv * D (half for causal), against
     # the 2.5 PFLOP/s dense f16 MFMA peak
     def measure_attention(name, b, hq, hkv, lq, lk, d, causal, dtype="f16"):
+        if not wanted(name):
+            return
         def make():
             return (filled(dtype, (b, hq, lq, d), "normal", 7, 0, 0.0, 1.0),
                     filled(dtype, (b, hkv, lk, d), "normal", 7, 1, 0.0, 1.0),
@@ -400,101 +591,116 @@ COPY_BYTES = 256 << 20  # calibration copy for counter runs: 256 MiB read + 256 
 def pmc_probe(sdk, reps=3):
     """Workload for `rocprofv3 --pmc` runs: a plain 16-byte-vector copy of
     COPY_BYTES (known traffic, the calibration for FETCH_SIZE / WRITE_SIZE),
-    then each cfg2 kernel, `reps` times each, with a 600 MB cache-flushing
-    write between dispatches so that every dispatch starts from HBM."""
-    from inference_c_amd import TensorView
-    n = COPY_BYTES // 2
-    src, dst = sdk.tensor("f16", (n,)), sdk.tensor("f16", (n,))
-    flush = sdk.tensor("f32", (ROTATE_BYTES // 4,))
-    sdk.call("tensor_fill_normal", src, 1, 9, 0.0, 1.0)
-    t = {}
-    t["x"], t["y"] = sdk.tensor("f16", (8192, 8192)), sdk.tensor("f16", (8192, 8192))
-    t["a"], t["b"], t["o"] = (sdk.tensor("f16", (4096, 16384)) for _ in range(3))
-    sdk.call("tensor_fill_normal", t["x"], 1, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["a"], 1, 1, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["b"], 1, 2, 0.0, 1.0)
-    view = TensorView.make((n,), (1,), 0)
-    ops = [("copy_f16", lambda: sdk.call("tensor_view_add_mul_f16", src, view, None, None, dst)),
-           ("silu_f16", lambda: sdk.call("tensor_silu_f16", t["x"], t["y"])),
-           ("gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x"], t["y"])),
-           ("swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b"], t["a"], t["o"]))]
-    # the Q8_0 decode GEMV of the suite: [28672, 8192] packed weights, one row
+    then every kernel of the bench step and the suite at its BASELINE shape,
+    under the suite's names, `reps` times each, with a 600 MB cache-flushing
+    write before each dispatch so that every dispatch starts from HBM, and a
+    synchronisation before it, so that under `--kernel-trace` each op's
+    duration is its execution from an idle GPU."""
     import numpy as np
-    packed = np.random.default_rng(7).integers(0, 256, size=(28672, 256, 34), dtype=np.uint8)
-    packed[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
-    t["w8"] = sdk.tensor("u8", packed.shape).upload(packed)
-    t["x8"], t["y8"] = sdk.tensor("f16", (1, 8192)), sdk.tensor("f16", (1, 28672))
-    sdk.call("tensor_fill_normal", t["x8"], 7, 3, 0.0, 1.0)
-    del packed
-    ops.append(("linear_q8_0_f16_1x8192_to_28672",
-                lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
-    # the configs[2..4] kernels at their BASELINE shapes
-    t["x3"], t["y3"] = sdk.tensor("f16", (16384, 2048)), sdk.tensor("f16", (16384, 2048))
-    t["w3"] = sdk.tensor("f16", (2048,))
-    sdk.call("tensor_fill_normal", t["x3"], 3, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_uniform", t["w3"], 3, 1, 0.5, 1.5)
-    ops.append(("cfg3_rms_norm_f16", lambda: sdk.call("tensor_rms_norm_f16", t["x3"], t["w3"],
-                                                      1e-6, t["y3"])))
-    t["lg"], t["sm"] = sdk.tensor("f16", (32, 2048, 2048)), sdk.tensor("f16", (32, 2048, 2048))
-    t["rs"] = sdk.tensor("f32", (32, 2048))
-    sdk.call("tensor_fill_normal", t["lg"], 3, 2, 0.0, 3.0)
-    ops.append(("cfg3_causal_softmax_f16", lambda: sdk.call("tensor_softmax_f16", t["lg"], 1,
-                                                            t["sm"])))
-    ops.append(("cfg3_row_sum_f16", lambda: sdk.call("tensor_row_sum_f16", t["lg"], t["rs"])))
-    ops.append(("cfg3_row_max_f16", lambda: sdk.call("tensor_row_max_f16", t["lg"], t["rs"])))
+    from inference_c_amd import TensorView
+    T = sdk.tensor
+
+    def filled(dtype, shape, kind, seed, stream_id, a, b):
+        x = T(dtype, shape)
+        sdk.call("tensor_fill_" + kind, x, seed, stream_id, a, b)
+        return x
+
+    n = COPY_BYTES // 2
+    src, dst = filled("f16", (n,), "normal", 1, 9, 0.0, 1.0), T("f16", (n,))
+    flush = T("f32", (ROTATE_BYTES // 4,))
+    flat = TensorView.make((n,), (1,), 0)
+    t = {}
+    ops = [("copy_f16", lambda: sdk.call("tensor_view_add_mul_f16", src, flat, None, None, dst))]
+    # cfg1
+    t["a1"] = filled("f32", (1024, 4096), "uniform", 0, 0, -1.0, 1.0)
+    t["b1"] = filled("f32", (1024, 4096), "uniform", 0, 1, -1.0, 1.0)
+    t["c1"], t["o1"] = filled("f32", (4096,), "uniform", 0, 2, -1.0, 1.0), T("f32", (1024, 4096))
+    ops += [("cfg1_add_f32", lambda: sdk.call("tensor_add_f32", t["a1"], t["b1"], t["o1"])),
+            ("cfg1_mul_f32", lambda: sdk.call("tensor_mul_f32", t["a1"], t["b1"], t["o1"])),
+            ("cfg1_bias_add_f32", lambda: sdk.call("tensor_bias_add_f32", t["a1"], t["c1"],
+                                                   t["o1"]))]
+    # cfg2
+    t["x2"], t["y2"] = filled("f16", (8192, 8192), "normal", 1, 0, 0.0, 1.0), T("f16", (8192, 8192))
+    t["a2"] = filled("f16", (4096, 16384), "normal", 1, 1, 0.0, 1.0)
+    t["b2"] = filled("f16", (4096, 16384), "normal", 1, 2, 0.0, 1.0)
+    t["o2"] = T("f16", (4096, 16384))
+    ops += [("cfg2_silu_f16", lambda: sdk.call("tensor_silu_f16", t["x2"], t["y2"])),
+            ("cfg2_gelu_f16", lambda: sdk.call("tensor_gelu_f16", t["x2"], t["y2"])),
+            ("cfg2_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["b2"], t["a2"],
+                                                 t["o2"]))]
+    # cfg3
+    t["x3"], t["y3"] = filled("f16", (16384, 2048), "normal", 3, 0, 0.0, 1.0), T("f16", (16384, 2048))
+    t["w3"] = filled("f16", (2048,), "uniform", 3, 1, 0.5, 1.5)
+    t["lg"], t["sm"] = filled("f16", (32, 2048, 2048), "normal", 3, 2, 0.0, 3.0), T("f16", (32, 2048, 2048))
+    t["rs"] = T("f32", (32, 2048))
+    ops += [("cfg3_rms_norm_f16", lambda: sdk.call("tensor_rms_norm_f16", t["x3"], t["w3"], 1e-6,
+                                                   t["y3"])),
+            ("cfg3_causal_softmax_f16", lambda: sdk.call("tensor_softmax_f16", t["lg"], 1, t["sm"])),
+            ("cfg3_row_sum_f16", lambda: sdk.call("tensor_row_sum_f16", t["lg"], t["rs"])),
+            ("cfg3_row_max_f16", lambda: sdk.call("tensor_row_max_f16", t["lg"], t["rs"]))]
+    # cfg4
     B, S, H, D = 16, 1024, 32, 64
     perm = TensorView.make((B, H, S, D), (S * H * D, D, H * D, 1), 0)
-    t["x4"], t["o4"] = sdk.tensor("f16", (B, S, H, D)), sdk.tensor("f16", (B, H, S, D))
-    t["a4"], t["m4"] = sdk.tensor("f16", (1, H, 1, D)), sdk.tensor("f16", (B, 1, S, 1))
-    sdk.call("tensor_fill_normal", t["x4"], 4, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_uniform", t["a4"], 4, 1, -1.0, 1.0)
-    sdk.call("tensor_fill_uniform", t["m4"], 4, 2, -1.0, 1.0)
+    t["x4"], t["o4"] = filled("f16", (B, S, H, D), "normal", 4, 0, 0.0, 1.0), T("f16", (B, H, S, D))
+    t["a4"] = filled("f16", (1, H, 1, D), "uniform", 4, 1, -1.0, 1.0)
+    t["m4"] = filled("f16", (B, 1, S, 1), "uniform", 4, 2, -1.0, 1.0)
     ops.append(("cfg4_permuted_broadcast_f16", lambda: sdk.call(
         "tensor_view_add_mul_f16", t["x4"], perm, t["a4"], t["m4"], t["o4"])))
-    t["x5"], t["r5"] = sdk.tensor("f16", (4096, 2048)), sdk.tensor("f16", (4096, 2048))
-    t["h5"], t["n5"] = sdk.tensor("f16", (4096, 2048)), sdk.tensor("f16", (4096, 2048))
-    sdk.call("tensor_fill_normal", t["x5"], 5, 0, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["r5"], 5, 1, 0.0, 1.0)
-    ops.append(("cfg5_residual_rms_norm_f16", lambda: sdk.call(
-        "tensor_residual_rms_norm_f16", t["x5"], t["r5"], t["w3"], 1e-6, t["h5"], t["n5"])))
+    # cfg5: the bench step's four calls
+    tok, hid, inter = 4096, 2048, 8192
+    t["x5"] = filled("f16", (tok, hid), "normal", 5, 0, 0.0, 1.0)
+    t["r5"] = filled("f16", (tok, hid), "normal", 5, 1, 0.0, 1.0)
+    t["w5"] = filled("f16", (hid,), "normal", 5, 9, 0.0, 1.0)
+    t["h5"], t["n5"] = T("f16", (tok, hid)), T("f16", (tok, hid))
+    t["q5"] = filled("f16", (tok, 32, 64), "normal", 5, 2, 0.0, 1.0)
+    t["k5"] = filled("f16", (tok, 32, 64), "normal", 5, 3, 0.0, 1.0)
+    t["g5"] = filled("f16", (tok, inter), "normal", 5, 4, 0.0, 1.0)
+    t["u5"], t["o5"] = filled("f16", (tok, inter), "normal", 5, 5, 0.0, 1.0), T("f16", (tok, inter))
+    t["big"] = filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0)
+    t["gs"], t["gm"] = T("f64", (1,)), T("f32", (1,))
+    ops += [("cfg5_residual_rms_norm_f16", lambda: sdk.call(
+                "tensor_residual_rms_norm_f16", t["x5"], t["r5"], t["w5"], 1e-6, t["h5"], t["n5"])),
+            ("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", t["q5"], t["k5"], 32, 32, 64,
+                                               10000.0, 0)),
+            ("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["g5"], t["u5"],
+                                                 t["o5"])),
+            ("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", t["big"], t["gs"],
+                                                         t["gm"]))]
+    # embedding gather: 32768 int32 ids into a [32000, 2048] f16 table
     vocab, width, tokens = 32000, 2048, 32768
-    t["emb"], t["eo"] = sdk.tensor("f16", (vocab, width)), sdk.tensor("f16", (tokens, width))
-    sdk.call("tensor_fill_normal", t["emb"], 6, 0, 0.0, 1.0)
-    t["ids"] = sdk.tensor("i32", (tokens,)).upload(
+    t["emb"], t["eo"] = filled("f16", (vocab, width), "normal", 6, 0, 0.0, 1.0), T("f16", (tokens, width))
+    t["ids"] = T("i32", (tokens,)).upload(
         ((np.arange(tokens, dtype=np.int64) * 2654435761) % vocab).astype(np.int32))
     ops.append(("embedding_lookup_f16", lambda: sdk.call("tensor_embedding_lookup_f16", t["emb"],
                                                          t["ids"], t["eo"])))
-    # kernels that stage data in LDS, for the LDS instruction / bank-conflict
-    # pass: RoPE (angle table), a [4096, 4096] f16 transpose (64x64 tiles),
-    # the global sum/max (cross-wave combine) and flash attention f16 / f32
-    t["q5"], t["k5"] = sdk.tensor("f16", (4096, 32, 64)), sdk.tensor("f16", (4096, 32, 64))
-    sdk.call("tensor_fill_normal", t["q5"], 5, 2, 0.0, 1.0)
-    sdk.call("tensor_fill_normal", t["k5"], 5, 3, 0.0, 1.0)
-    ops.append(("rope_f16", lambda: sdk.call("tensor_rope_f16", t["q5"], t["k5"], 32, 32, 64,
-                                             10000.0, 0)))
-    t["xt"], t["yt"] = sdk.tensor("f16", (4096, 4096)), sdk.tensor("f16", (4096, 4096))
-    sdk.call("tensor_fill_normal", t["xt"], 4, 0, 0.0, 1.0)
+    # the Q8_0 decode GEMV of the suite: [28672, 8192] packed weights, one row
+    packed = np.random.default_rng(7).integers(0, 256, size=(28672, 256, 34), dtype=np.uint8)
+    packed[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
+    t["w8"] = T("u8", packed.shape).upload(packed)
+    t["x8"], t["y8"] = filled("f16", (1, 8192), "normal", 7, 3, 0.0, 1.0), T("f16", (1, 28672))
+    del packed
+    ops.append(("linear_q8_0_f16_1x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
+    # a [4096, 4096] f16 transpose (64x64 LDS tiles)
+    t["xt"], t["yt"] = filled("f16", (4096, 4096), "normal", 4, 0, 0.0, 1.0), T("f16", (4096, 4096))
     transpose = TensorView.make((4096, 4096), (1, 4096), 0)
     ops.append(("transpose_f16", lambda: sdk.call("tensor_view_add_mul_f16", t["xt"], transpose,
                                                   None, None, t["yt"])))
-    t["g"] = sdk.tensor("f32", (1 << 28,))
-    t["gs"], t["gm"] = sdk.tensor("f64", (1,)), sdk.tensor("f32", (1,))
-    sdk.call("tensor_fill_uniform", t["g"], 0, 5, -1.0, 1.0)
-    ops.append(("global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", t["g"], t["gs"],
-                                                       t["gm"])))
+    # prefill attention, f16 and f32, 32 q-heads / 8 kv-heads, 2048^2, D 128, causal
     for dtype in ("f16", "f32"):
-        qa = sdk.tensor(dtype, (1, 32, 2048, 128))
-        ka, va = sdk.tensor(dtype, (1, 8, 2048, 128)), sdk.tensor(dtype, (1, 8, 2048, 128))
-        oa = sdk.tensor(dtype, (1, 32, 2048, 128))
-        for i, x in enumerate((qa, ka, va)):
-            sdk.call("tensor_fill_normal", x, 6, i, 0.0, 1.0)
-        t["attn_" + dtype] = (qa, ka, va, oa)
+        qa = filled(dtype, (1, 32, 2048, 128), "normal", 6, 0, 0.0, 1.0)
+        ka = filled(dtype, (1, 8, 2048, 128), "normal", 6, 1, 0.0, 1.0)
+        va = filled(dtype, (1, 8, 2048, 128), "normal", 6, 2, 0.0, 1.0)
+        t["attn_" + dtype] = (qa, ka, va, T(dtype, (1, 32, 2048, 128)))
         ops.append((f"sdpa_{dtype}_prefill", lambda d=dtype: sdk.call(
             f"tensor_sdpa_device_{d}", *t["attn_" + d][:3], None, 0.08838834764831845, 1,
             t["attn_" + d][3])))
     for name, fn in ops:
         for _ in range(reps):
             sdk.call("tensor_fill_uniform", flush, 7, 0, -1.0, 1.0)
+            # the op starts on an idle GPU: under --kernel-trace its duration
+            # is its own execution, without the wait behind a previous kernel
+            sdk.synchronize()
             fn()
             sdk.synchronize()
         print(f"pmc probe: {name} x{reps}", flush=True)
@@ -503,13 +709,13 @@ def pmc_probe(sdk, reps=3):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only run the counter-collection workload (copy, cfg2 kernels and "
-                         "the Q8_0 decode GEMV)")
+                    help="only run the counter-collection workload (a calibration copy, then "
+                         "every step and suite kernel at its BASELINE shape)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one "
@@ -527,85 +733,106 @@ def main():
     hip = Hip()
     stream = sdk.stream()
 
-    # Each kernel gets its own rotation of identical operand sets, at least
-    # 600 MB apart in traffic, so no launch finds its operands in the 256 MB
-    # last-level cache.
-    def filled(dtype, shape, stream_id):
+    # configs[4] operands, seed 5 (chain) and seed 0 (global), one set: the
+    # step's 4 GiB global read flushes the last-level cache between chains.
+    tok, hid, inter = 4096, 2048, 8192
+
+    def filled(dtype, shape, kind, seed, stream_id, a, b):
         x = sdk.tensor(dtype, shape)
-        sdk.call("tensor_fill_normal", x, 1, stream_id, 0.0, 1.0)
+        sdk.call("tensor_fill_" + kind, x, seed, stream_id, a, b)
         return x
 
-    def unary_sets():
-        return [(filled("f16", (8192, 8192), 0), sdk.tensor("f16", (8192, 8192)))
-                for _ in range(3)]
-
-    silu_sets, gelu_sets = unary_sets(), unary_sets()
-    swiglu_sets = [(filled("f16", (4096, 16384), 1), filled("f16", (4096, 16384), 2),
-                    sdk.tensor("f16", (4096, 16384))) for _ in range(2)]
+    t = {"x": filled("f16", (tok, hid), "normal", 5, 0, 0.0, 1.0),
+         "r": filled("f16", (tok, hid), "normal", 5, 1, 0.0, 1.0),
+         "w": filled("f16", (hid,), "normal", 5, 9, 0.0, 1.0),
+         "h": sdk.tensor("f16", (tok, hid)), "n": sdk.tensor("f16", (tok, hid)),
+         "q": filled("f16", (tok, 32, 64), "normal", 5, 2, 0.0, 1.0),
+         "k": filled("f16", (tok, 32, 64), "normal", 5, 3, 0.0, 1.0),
+         "g": filled("f16", (tok, inter), "normal", 5, 4, 0.0, 1.0),
+         "u": filled("f16", (tok, inter), "normal", 5, 5, 0.0, 1.0),
+         "o": sdk.tensor("f16", (tok, inter)),
+         "big": filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0),
+         "sum": sdk.tensor("f64", (1,)), "max": sdk.tensor("f32", (1,))}
     sdk.synchronize()
-    phases = [
-        ("silu_f16", lambda i: sdk.call("tensor_silu_f16", *silu_sets[i % 3])),
-        ("gelu_f16", lambda i: sdk.call("tensor_gelu_f16", *gelu_sets[i % 3])),
-        # out = a * silu(b): b is the SiLU'd (gate) operand, a the up operand
-        ("swiglu_f16", lambda i: sdk.call("tensor_silu_multiply_f16", swiglu_sets[i % 2][1],
-                                          swiglu_sets[i % 2][0], swiglu_sets[i % 2][2])),
+    calls = [
+        ("cfg5_residual_rms_norm_f16", lambda: sdk.call("tensor_residual_rms_norm_f16", t["x"], t["r"],
+                                                   t["w"], 1e-6, t["h"], t["n"])),
+        ("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", t["q"], t["k"], 32, 32, 64, 10000.0, 0)),
+        # out = up * silu(gate): the compute-table order, gate first
+        ("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["g"], t["u"], t["o"])),
+        ("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", t["big"], t["sum"],
+                                                t["max"])),
     ]
-    for i in range(args.warmup):
-        for _, fn in phases:
-            fn(i)
+    for _ in range(args.warmup):
+        for _, fn in calls:
+            fn()
     sdk.synchronize()
-    # Timed region: K launches of each kernel, back to back on the SDK
-    # stream, with one event before the first launch and one after each
-    # kernel's K launches: per-kernel average = its phase / K.
-    marks = [hip.event() for _ in range(len(phases) + 1)]
+    # Timed region: K steps back to back on the SDK stream. Events mark each
+    # step's start and the end of its chain (= the start of the global
+    # reduction): an event between two calls delays the second one's dispatch
+    # by a few microseconds, so the chain's three calls run back to back and
+    # are timed as one chain; their separate figures
+    # come from the suite.
+    marks = [hip.event() for _ in range(2 * args.steps + 1)]
     t0 = time.perf_counter()
-    hip.record(marks[0], stream)
-    for j, (_, fn) in enumerate(phases):
-        for i in range(args.steps):
-            fn(i)
-        hip.record(marks[j + 1], stream)
+    for i in range(args.steps):
+        hip.record(marks[2 * i], stream)
+        for _, fn in calls[:3]:
+            fn()
+        hip.record(marks[2 * i + 1], stream)
+        calls[3][1]()
+    hip.record(marks[-1], stream)
     sdk.synchronize()
     wall = time.perf_counter() - t0
-    per_kernel = {name: hip.elapsed_ms(marks[j], marks[j + 1]) / args.steps
-                  for j, (name, _) in enumerate(phases)}
+    chain_ms = statistics.fmean(hip.elapsed_ms(marks[2 * i], marks[2 * i + 1])
+                                for i in range(args.steps))
+    global_ms = statistics.fmean(hip.elapsed_ms(marks[2 * i + 1], marks[2 * i + 2])
+                                 for i in range(args.steps))
+    for v in t.values():
+        v.free()
 
-    step_bytes = sum(v[0] for v in CFG2.values())
-    step_elems = sum(v[1] for v in CFG2.values())
+    step_bytes = sum(v[0] for v in CFG5.values())
+    step_elems = CFG5_CHAIN_ELEMENTS + CFG5["cfg5_global_sum_max_f32"][1]
     ms_per_step = wall / args.steps * 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    dominant = max(per_kernel, key=per_kernel.get)
-    achieved = CFG2[dominant][0] / (per_kernel[dominant] * 1e-3) / 1e9
-    kernels = {name: {"avg_us": round(ms * 1e3, 2),
-                      "gbps": round(CFG2[name][0] / (ms * 1e-3) / 1e9, 1),
-                      "pct_peak": round(100 * CFG2[name][0] / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
-                      "elements_per_s": float(f"{CFG2[name][1] / (ms * 1e-3):.4g}")}
-               for name, ms in per_kernel.items()}
-    for group in (silu_sets, gelu_sets, swiglu_sets):
-        for tensors in group:
-            for v in tensors:
-                v.free()
+    chain_bytes = sum(v[0] for n, v in CFG5.items() if n != "cfg5_global_sum_max_f32")
+    global_bytes = CFG5["cfg5_global_sum_max_f32"][0]
+    achieved = global_bytes / (global_ms * 1e-3) / 1e9
 
+    def rates(nbytes, elements, ms):
+        return {"avg_us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "pct_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                "elements_per_s": float(f"{elements / (ms * 1e-3):.4g}"), "bytes": nbytes}
+    kernels = {"cfg5_decoder_chain_f16": rates(chain_bytes, CFG5_CHAIN_ELEMENTS, chain_ms),
+               "cfg5_global_sum_max_f32": rates(global_bytes, CFG5["cfg5_global_sum_max_f32"][1],
+                                                global_ms)}
+    kernels["cfg5_decoder_chain_f16"]["calls"] = [n for n, _ in calls[:3]]
     line = {
         "metric": "achieved HBM GB/s and % of MI355X peak per tensor_ops kernel; elements/sec",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-        "config": {"workload": "BASELINE configs[1]: SiLU + tanh-GELU on [8192,8192] f16 N(0,1) "
-                               "and SwiGLU a*silu(b) on [4096,16384] f16 N(0,1), seed 1, inputs "
-                               "resident in HBM", "step_bytes": step_bytes,
-                   "elements_per_step": step_elems},
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[4]: decoder-layer non-GEMM chain in f16 "
+                               "(fused residual add + RMSNorm eps 1e-6 on [4096,2048], RoPE "
+                               "theta 1e4 on q,k [4096,32,64] positions 0..4095, SwiGLU on "
+                               "[4096,8192]; all N(0,1), seed 5) then the global sum + max over "
+                               "2^30 f32 U[-1,1] (seed 0); inputs resident in HBM",
+                   "step_bytes": step_bytes, "elements_per_step": step_elems,
+                   "dtypes": "chain f16 (f32 arithmetic), global f32 (f64 sum)"},
         "pct_of_peak": round(100 * value / PEAK_GBPS, 1),
         "elements_per_s": float(f"{step_elems / (ms_per_step * 1e-3):.4g}"),
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-                     "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": measured_traffic(dominant),
-                     "algorithmic_bytes": CFG2[dominant][0]},
+        "roofline": {"bound": "hbm", "kernel": "tensor_sum_max_f32 (sum_max_pass1 + "
+                                              "sum_max_pass2, one call)",
+                     "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": measured_traffic("cfg5_global_sum_max_f32"),
+                     "algorithmic_bytes": global_bytes},
         "kernels": kernels,
     }
     if not args.no_suite:
         line["suite"] = suite(sdk, hip, stream)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_baseline(line.get("suite"), kernels)
     print(json.dumps(line), flush=True)
 
 

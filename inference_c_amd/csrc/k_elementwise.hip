@@ -106,9 +106,10 @@ __device__ inline Vec16<S> apply(const Vec16<S> &a, const Vec16<S> &b, Op op) {
 // operand). Measured on MI355X this streams at the device's practical
 // ceiling (~6.4 TB/s for 128 MiB operands); deeper per-lane unrolling and
 // persistent grid-stride loops were 5-20% slower, and cached (temporal)
-// loads ~40% slower. Vectors past the grid's coverage (grids are capped at
-// 2^31 - 1 blocks) are picked up by the stride loop, whose bound is
-// block-uniform. kThrough selects write-through stores (small outputs).
+// loads ~40% slower. A launch covers at most kMaxLaunchVecs vectors (a
+// dispatch's work-item count is 32 bits); the host splits longer operands
+// into several launches. kThrough selects write-through stores (small
+// outputs).
 template <typename S, int kArity, class Op, bool kThrough>
 __global__ __launch_bounds__(kBlock) void map_vec_kernel(const S *__restrict__ a,
                                                          const S *__restrict__ b,
@@ -151,12 +152,20 @@ __global__ __launch_bounds__(kBlock) void map_scalar_kernel(const S *__restrict_
 
 inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
+// Blocks for a grid-stride kernel: one lane per work item, capped so that
+// blocks * per_block work-items fit the dispatch's 32-bit count (the kernels
+// loop over the rest).
 unsigned grid_for(size_t work_items, size_t per_block) {
     size_t blocks = (work_items + per_block - 1) / per_block;
     if (blocks < 1) blocks = 1;
-    if (blocks > size_t{0x7fffffff}) blocks = size_t{0x7fffffff};
+    const size_t cap = size_t{0xffffffff} / per_block;
+    if (blocks > cap) blocks = cap;
     return (unsigned)blocks;
 }
+
+// Vectors per map_vec_kernel launch: a multiple of kBlock, with the work-item
+// count (blocks * kBlock) below 2^32.
+constexpr size_t kMaxLaunchVecs = size_t{1} << 31;
 
 template <typename S, int kArity, class Op>
 hipError_t launch_map(const S *a, const S *b, S *y, size_t n, hipStream_t s) {
@@ -164,15 +173,26 @@ hipError_t launch_map(const S *a, const S *b, S *y, size_t n, hipStream_t s) {
     constexpr int E = Vec16<S>::N;
     if (aligned16(a) && aligned16(b) && aligned16(y)) {
         const size_t nvec = n / E;
-        // map_vec_kernel covers nvec in one pass of the grid
-        if (nvec > size_t{0x7fffffff} * kBlock) return hipErrorInvalidValue;
-        const unsigned grid = grid_for(nvec > 0 ? nvec : 1, (size_t)kBlock);
-        if (write_through_for(n * sizeof(S)))
-            hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, true>), dim3(grid), dim3(kBlock),
-                               0, s, a, b, y, nvec, n, Op{});
-        else
-            hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, false>), dim3(grid), dim3(kBlock),
-                               0, s, a, b, y, nvec, n, Op{});
+        const bool through = write_through_for(n * sizeof(S));
+        // each launch covers its part of nvec in one pass of the grid; the
+        // last one also takes the ragged tail of fewer than E elements
+        size_t done = 0;
+        do {
+            const size_t part = nvec - done > kMaxLaunchVecs ? kMaxLaunchVecs : nvec - done;
+            const bool last = done + part == nvec;
+            const size_t part_n = last ? n - done * E : part * E;
+            const S *pa = a + done * E;
+            const S *pb = b == nullptr ? nullptr : b + done * E;
+            S *py = y + done * E;
+            const unsigned grid = (unsigned)((part > 0 ? part + kBlock - 1 : kBlock) / kBlock);
+            if (through)
+                hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, true>), dim3(grid), dim3(kBlock),
+                                   0, s, pa, pb, py, part, part_n, Op{});
+            else
+                hipLaunchKernelGGL((map_vec_kernel<S, kArity, Op, false>), dim3(grid),
+                                   dim3(kBlock), 0, s, pa, pb, py, part, part_n, Op{});
+            done += part;
+        } while (done < nvec);
     } else {
         hipLaunchKernelGGL((map_scalar_kernel<S, kArity, Op>), dim3(grid_for(n, kBlock)),
                            dim3(kBlock), 0, s, a, b, y, n, Op{});
@@ -256,8 +276,11 @@ hipError_t launch_bias(const S *x, const S *bias, S *y, size_t rows, size_t widt
     if (n == 0) return hipSuccess;
     constexpr int E = Vec16<S>::N;
     const size_t nvec = n / E;
+    // the vector kernel is one-shot: its grid must cover nvec within the
+    // dispatch's 32-bit work-item count; longer operands take the
+    // grid-stride scalar kernel
     if (width % E == 0 && aligned16(x) && aligned16(bias) && aligned16(y) &&
-        nvec < (size_t{1} << 32)) {
+        nvec <= kMaxLaunchVecs) {
         const dim3 grid(grid_for(nvec, kBlock)), block(kBlock);
         const FastDiv per_row = make_fast_div((uint32_t)(width / E));
         if (write_through_for(n * sizeof(S)))

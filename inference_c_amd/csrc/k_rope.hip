@@ -97,7 +97,13 @@ struct RopeDenoms {
 // Item = (position, row, chunk): row < qh is a q head, else a k head; chunk
 // c covers pairs c*E .. c*E+E-1. Items are numbered position-major; block
 // (x, y) owns items y*kIt*128 .. +kIt*128 of positions x*ppb ..
-// x*ppb+ppb-1 and computes those positions' rotations.
+// x*ppb+ppb-1 and computes those positions' rotations. Wave w of the block
+// takes the item groups w*kIt .. w*kIt+kIt-1 (32 items each), so its kIt
+// groups are consecutive: when a position has a multiple of 32*kIt items
+// (config 5: 256), all of a wave's items share one position and each lane
+// one chunk, and the lane reads its E rotations from LDS once instead of
+// once per item (a read is skipped whenever no lane of the wave needs a
+// different slot than for the previous group).
 //
 // Lanes l and l + 32 of a wave share an item: lane l < 32 moves the item's
 // left vector, lane l + 32 its right vector (half elements further on). A
@@ -115,6 +121,11 @@ struct RopeDenoms {
 // makes it wait for one item before requesting the next, and there is no
 // loop, so nothing waits for the loads before the rotations are computed.
 constexpr uint32_t kPairItems = kBlock / 2;   // items per block and per kIt
+
+// Items per lane pair the host aims for (1, 2, 4 or 8).
+#ifndef ICSDK_ROPE_ITEMS
+#define ICSDK_ROPE_ITEMS 8
+#endif
 
 template <typename S, int kChunks, int kIt>
 __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S *__restrict__ k,
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     S *const k0 = k + (size_t)p0 * kh * (2 * half);
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
-        const uint32_t raw = it0 + (u * (kBlock / kWave) + wave) * 32 + (lane & 31);
+        const uint32_t raw = it0 + (wave * kIt + u) * 32 + (lane & 31);
         ok[u] = raw < items;
         const uint32_t item = ok[u] ? raw : 0u;
         // multiply-high division: a 32-bit divide by the run-time per_pos was
@@ -178,8 +189,14 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     // results go back through L2 (write-through stores) into the same bytes
     const OutWindow q_out(q0, npos * qh * (2 * half) * (uint32_t)sizeof(S));
     const OutWindow k_out(k0, npos * kh * (2 * half) * (uint32_t)sizeof(S));
+    float2 t[E];   // the rotations of the lane's current slot
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
+        // wave-uniform: read the rotations unless every lane keeps its slot
+        if (u == 0 || __builtin_amdgcn_ballot_w64(slot[u] != slot[u - 1]) != 0) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) t[e] = rot[slot[u] + e];
+        }
         // every lane takes part in the swap (a lane past the end holds item 0)
         const uint4 words = __builtin_bit_cast(uint4, v[u]);
         const uint32_t w[4] = {words.x, words.y, words.z, words.w};
@@ -196,10 +213,9 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
         Vec16<S> out;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const float2 t = rot[slot[u] + e];
             const float l = Elem<S>::load(lv.v[e]), r = Elem<S>::load(rv.v[e]);
-            const float a = side ? r : l, b = side ? l : r, sb = side ? t.y : -t.y;
-            out.v[e] = Elem<S>::store(a * t.x + b * sb);
+            const float a = side ? r : l, b = side ? l : r, sb = side ? t[e].y : -t[e].y;
+            out.v[e] = Elem<S>::store(a * t[e].x + b * sb);
         }
         // The window is chosen per wave (a descriptor must be wave-uniform):
         // a wave whose items all lie in q, or all in k, writes through its
@@ -251,7 +267,7 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
         // (the loads of 8 items in flight per lane measured fastest at the
         // BASELINE shape: 4 positions of 64 rows x 4 chunks, 14.4 -> 13.0 us),
         // and at most kLdsPairs rotations
-        constexpr size_t kTargetIt = 8;
+        constexpr size_t kTargetIt = ICSDK_ROPE_ITEMS;
         const size_t per_pos = heads * chunks;
         size_t ppb = per_pos >= kTargetIt * kPairItems ? 1 : kTargetIt * kPairItems / per_pos;
         if (ppb * half > (size_t)kLdsPairs) ppb = (size_t)kLdsPairs / half;

@@ -544,11 +544,17 @@ struct RowShape {
     int wpr;
 };
 
+// Waves per row tried first (1 or 4): the narrowest row group whose lanes
+// hold the row in at most 8 vectors each wins.
+#ifndef ICSDK_ROW_WPR_FIRST
+#define ICSDK_ROW_WPR_FIRST 1
+#endif
+
 inline bool pick_row_shape(size_t width, size_t elem, bool aligned, RowShape *shape) {
     const size_t per_vec = 16 / elem;
     if (!aligned || width == 0 || width % per_vec != 0 || width > 0xffffffffu) return false;
     const size_t vpr = width / per_vec;
-    for (int wpr : {1, 4}) {
+    for (int wpr : {ICSDK_ROW_WPR_FIRST, 5 - ICSDK_ROW_WPR_FIRST}) {
         const size_t threads = (size_t)wpr * kWave;
         for (int nv : {1, 2, 4, 8}) {
             if ((size_t)nv * threads >= vpr) {

@@ -227,6 +227,10 @@ bool short_plan(const Coalesced &c, uint64_t x_offset, uint64_t n, ShortPlan *pl
     const int last = c.rank - 1;
     const int outer_rank = c.rank >= 2 ? c.rank - 2 : 0;
     if (outer_rank > 2 || n > 0xffffffffull) return false;
+    // offsets are unsigned 32-bit sums: a negative stride would make the
+    // reach below wrap (and the base offset be truncated) undetected
+    for (int d = 0; d < c.rank; ++d)
+        if (c.x_stride[d] < 0) return false;
     const uint64_t vecs = c.shape[last] / E;
     const uint64_t rows = c.rank >= 2 ? c.shape[last - 1] : 1;
     const uint64_t plane = rows * vecs;
@@ -374,6 +378,8 @@ bool gather_plan(const Coalesced &c, uint64_t x_offset, uint64_t n, bool have_a,
     constexpr uint64_t E = Vec16<S>::N;
     const int last = c.rank - 1;
     if (c.x_stride[last] != 1 || c.shape[last] % E != 0 || x_offset % E != 0) return false;
+    for (int d = 0; d < last; ++d)
+        if (c.x_stride[d] < 0) return false;  // offsets are unsigned sums
     const bool a_vec = have_a && c.a_stride[last] != 0;
     const bool m_vec = have_m && c.m_stride[last] != 0;
     for (int d = 0; d < last; ++d) {

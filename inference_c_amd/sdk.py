@@ -202,6 +202,16 @@ class Tensor:
             raise SdkError(err.value.decode())
         return out
 
+    def download_range(self, first: int, count: int) -> np.ndarray:
+        """Elements first .. first + count - 1 of the flattened tensor."""
+        dt = np.dtype(NUMPY_DTYPES[self.dtype])
+        out = np.empty(count, dtype=dt)
+        err = ctypes.create_string_buffer(512)
+        if out.nbytes and not self.sdk.lib.tensor_buffer_download(
+                self.handle, first * dt.itemsize, out.ctypes.data, out.nbytes, err, 512):
+            raise SdkError(err.value.decode())
+        return out
+
     def free(self) -> None:
         if self.handle:
             self.sdk.lib.tensor_buffer_free(self.handle)

@@ -203,3 +203,26 @@ def test_config2_full_size(sdk, orc):
     out = sdk.tensor("f16", (4096, 16384))
     sdk.call("tensor_silu_multiply_f16", b, a, out)  # out = a * silu(b)
     assert_f16_ulps(out.download(), orc.silu_multiply(b.download(), a.download()), 1, "swiglu cfg2")
+
+
+def test_add_f16_past_one_launch(sdk, orc):
+    """2^34 + 43 f16 elements: more than 2^31 16-byte vectors, past what one
+    one-shot launch may cover (a dispatch counts its work-items in 32 bits),
+    so the map is split over launches. The start, both sides of the seam
+    between the launches and the ragged tail are bit-exact (96 GiB of device
+    operands; the windows are read back and checked against the oracle's
+    fill of the same element indices)."""
+    n = (1 << 34) + 8 * 5 + 3
+    print(f"f16 add past one launch: {n} elements", flush=True)
+    a, b, y = sdk.tensor("f16", (n,)), sdk.tensor("f16", (n,)), sdk.tensor("f16", (n,))
+    sdk.call("tensor_fill_normal", a, 21, 0, 0.0, 1.0)
+    sdk.call("tensor_fill_normal", b, 21, 1, 0.0, 1.0)
+    sdk.call("tensor_residual_add_f16", a, b, y)
+    sdk.synchronize()
+    seam = (1 << 31) * 8
+    for first in (0, seam - 4096, n - 4096):
+        want = orc.add(orc.normal((4096,), 21, 0, 0.0, 1.0, first=first),
+                       orc.normal((4096,), 21, 1, 0.0, 1.0, first=first))
+        assert_bits_equal(y.download_range(first, 4096), want)
+    for t in (a, b, y):
+        t.free()

@@ -243,6 +243,23 @@ def test_validation_precedes_device_use(lib):
         assert not ok and msg == message, (args[0], msg)
 
 
+def test_view_refuses_negative_strides_and_views_outside_the_input(lib):
+    """The strided-view kernels address x with unsigned offsets, so the entry
+    point refuses negative strides (and views reaching past the input) before
+    any device work, whatever the offset."""
+    from inference_c_amd import Sdk, TensorView
+    sdk = Sdk()
+    x = sdk.tensor("f16", (4, 64), device=False)
+    y = sdk.tensor("f16", (2, 64), device=False)
+    message = ("view add/mul requires non-negative strides, a view that lies inside the input, "
+               "and an output of the view's shape")
+    for view in (TensorView.make((2, 64), (-64, 1), 128),
+                 TensorView.make((2, 64), (-64, 1), (1 << 32) + 64),
+                 TensorView.make((2, 64), (64, 1), 192)):
+        ok, msg = sdk.try_call("tensor_view_add_mul_f16", x, view, None, None, y)
+        assert not ok and msg == message
+
+
 def test_embedding_validation_matches_reference(lib, ref, orc):
     """tensor_embedding_lookup_* reject bad operands and bad indices with the
     reference's messages (src/common/tensor_ops.c:86-161) before any device

@@ -163,6 +163,74 @@ def test_rng_definition(orc):
     assert_bits_equal(h, orc.normal((1000,), 9, 4, 0.0, 3.0, "f32").astype(F16), "f16 = rne(f32)")
 
 
+_M64 = (1 << 64) - 1
+_GAMMA = 0x9E3779B97F4A7C15
+
+
+def _splitmix64(state: int, k: int) -> int:
+    """Output k (k >= 1) of splitmix64 seeded with `state` (Steele, Lea and
+    Flood, OOPSLA 2014; Vigna's splitmix64.c): state advances by the golden
+    gamma, the output is the mixed state."""
+    z = (state + _GAMMA * k) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def test_rng_bits_pinned_to_published_splitmix64():
+    """The fills' generator, pinned without the oracle's code: this file's
+    splitmix64 reproduces the published output sequences (seed 1234567:
+    6457827717110365317, 3203168211198807973, 9817491932198370423,
+    4593380528125082431, 16408922859458223821; seed 0: 0xE220A8397B1DCDAF),
+    and orc_rng_bits(seed, stream, i) is output i + 1 of the generator whose
+    state is output 2*stream + 1 of the generator seeded `seed` (one
+    independent splitmix64 stream per (seed, tensor), indexed by element)."""
+    import ctypes
+    from oracle import ORACLE_PATH
+    assert [_splitmix64(1234567, k) for k in range(1, 6)] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423,
+        4593380528125082431, 16408922859458223821]
+    assert _splitmix64(0, 1) == 0xE220A8397B1DCDAF
+    lib = ctypes.CDLL(ORACLE_PATH)
+    lib.orc_rng_bits.argtypes = [ctypes.c_uint64] * 3
+    lib.orc_rng_bits.restype = ctypes.c_uint64
+    for seed, stream, index in [(0, 0, 0), (1, 2, 3), (5, 9, 123456789), (2**63 + 7, 1, 2**40),
+                                (9, 4, 0)]:
+        key = _splitmix64(seed, 2 * stream + 1)
+        assert lib.orc_rng_bits(seed, stream, index) == _splitmix64(key, index + 1)
+
+
+def test_rng_value_maps_from_the_definition(orc):
+    """U[low, high] = low + (high - low) * (top 24 bits * 2^-24) in f32;
+    N(mean, std) by Box-Muller in double on u1 = (bits >> 11 + 1) * 2^-53 in
+    (0, 1] and u2 = (second >> 11) * 2^-53 in [0, 1), second = the mixed
+    bits ^ 0xD1B54A32D192ED03, then f32, then f16 by RNE. Evaluated here
+    with Python's float (C double, the C library's log/cos/sqrt) and
+    numpy's f32 rounding, from splitmix64 pinned above."""
+    import math
+    def mix(z):
+        return _splitmix64((z - _GAMMA) & _M64, 1)
+    seed, stream, n = 11, 3, 2000
+    key = _splitmix64(seed, 2 * stream + 1)
+    bits = [_splitmix64(key, i + 1) for i in range(n)]
+    low, high = np.float32(-1.5), np.float32(2.25)
+    want_u = np.array([low + (high - low) * (np.float32(b >> 40) * np.float32(2.0 ** -24))
+                       for b in bits], np.float32)
+    assert_bits_equal(orc.uniform((n,), seed, stream, -1.5, 2.25), want_u, "uniform f32")
+    mean, std = float(np.float32(0.25)), float(np.float32(3.0))
+    want_n = []
+    for b in bits:
+        second = mix(b ^ 0xD1B54A32D192ED03)
+        u1 = ((b >> 11) + 1) * 2.0 ** -53
+        u2 = (second >> 11) * 2.0 ** -53
+        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(6.283185307179586 * u2)
+        want_n.append(np.float32(mean + std * z))
+    want_n = np.array(want_n, np.float32)
+    assert_bits_equal(orc.normal((n,), seed, stream, 0.25, 3.0, "f32"), want_n, "normal f32")
+    assert_bits_equal(orc.normal((n,), seed, stream, 0.25, 3.0, "f16"), want_n.astype(F16),
+                      "normal f16")
+
+
 def test_residual_rms_norm_is_add_then_norm(orc):
     x = orc.normal((8, 64), 10, 0, 0.0, 1.0)
     r = orc.normal((8, 64), 10, 1, 0.0, 1.0)
