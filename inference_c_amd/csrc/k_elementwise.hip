@@ -54,7 +54,12 @@ constexpr float kGeluC2 = (float)((double)kGeluC1 * (double)0.044715f);
 template <bool kFast>
 __device__ inline float gelu(float v) {
     if constexpr (kFast) {
-        const float t = v * __builtin_fmaf(kGeluC2, v * v, kGeluC1);
+        // The two products as fmas with a zero addend (equal to the plain
+        // products but for the sign of an exact zero, which exp2 ignores):
+        // each then reads an f16 input straight from its packed register
+        // (v_fma_mix_f32), with no separate conversion to f32.
+        const float v2 = __builtin_fmaf(v, v, 0.0f);
+        const float t = __builtin_fmaf(v, __builtin_fmaf(kGeluC2, v2, kGeluC1), 0.0f);
         const float r = v * fast_rcp(1.0f + __builtin_amdgcn_exp2f(t));
         return v <= -5.0f ? 0.0f : r;
     } else {
@@ -66,7 +71,11 @@ __device__ inline float gelu(float v) {
 
 template <bool kFast>
 __device__ inline float silu(float v) {
-    if constexpr (kFast) return v * fast_rcp(1.0f + fast_exp(-v));
+    // -v log2(e) as an fma with a zero addend: v_fma_mix_f32 reads the f16
+    // input directly (same value as the product; exp2 ignores a zero's sign)
+    if constexpr (kFast)
+        return v * fast_rcp(1.0f + __builtin_amdgcn_exp2f(
+                                       __builtin_fmaf(v, -1.4426950408889634f, 0.0f)));
     else return v / (1.0f + expf(-v));
 }
 

@@ -44,6 +44,39 @@ def test_rms_norm_f32(sdk, orc, rows, width):
     assert_f32_rel(ty.download(), orc.rms_norm(x, w, 1e-6), 1e-5, "rms f32")
 
 
+@pytest.mark.parametrize("dtype,rows,width", [
+    ("f16", 8192, 2048),    # four waves per row, exact rows
+    ("f16", 8200, 2056),    # four waves per row, 257 vectors (two per lane, ragged)
+    ("f16", 9000, 64),      # many narrow rows: one wave per row
+    ("f32", 8192, 1024),    # four waves per row, f32
+    ("f16", 8191, 2048),    # just under the row threshold: one wave per row
+])
+def test_rms_norm_many_rows(sdk, orc, dtype, rows, width):
+    """From 8192 rows of at least 256 vectors RMSNorm launches four waves per
+    row; both sides of the rule, exact and ragged rows, f16 and f32, plain and
+    with the residual."""
+    if dtype == "f16":
+        x = orc.normal((rows, width), 24, 0, 0.0, 1.0)
+        r = orc.normal((rows, width), 24, 1, 0.0, 1.0)
+        w = orc.uniform((width,), 24, 2, 0.5, 1.5, "f16")
+    else:
+        x = orc.normal((rows, width), 24, 0, 0.0, 1.0, "f32")
+        w = orc.uniform((width,), 24, 2, 0.5, 1.5)
+    tx, tw = tensors(sdk, [x, w])
+    ty = sdk.tensor(dtype, x.shape)
+    sdk.call(f"tensor_rms_norm_{dtype}", tx, tw, 1e-6, ty)
+    if dtype == "f16":
+        assert_f16_ulps(ty.download(), orc.rms_norm(x, w, 1e-6), 1, "rms f16")
+        tr = sdk.from_numpy(r)
+        ts, tn = sdk.tensor("f16", x.shape), sdk.tensor("f16", x.shape)
+        sdk.call("tensor_residual_rms_norm_f16", tx, tr, tw, 1e-6, ts, tn)
+        s_ref, y_ref = orc.residual_rms_norm(x, r, w, 1e-6)
+        assert_bits_equal(ts.download(), s_ref, "sum")
+        assert_f16_ulps(tn.download(), y_ref, 1, "norm of sum")
+    else:
+        assert_f32_rel(ty.download(), orc.rms_norm(x, w, 1e-6), 1e-5, "rms f32")
+
+
 def test_rms_norm_known_answer(sdk):
     # reference tests/test_tensor_ops.c:84-97
     tx = sdk.from_numpy(np.array([[3, 4], [0, 2]], np.float32))
