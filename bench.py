@@ -387,6 +387,22 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
                                   "pct_peak_traffic": round(100 * traffic / (best * 1e-3) / 1e9
                                                             / PEAK_GBPS, 1)})
 
+    # the host's per-call cost through this Python binding: a 64-element f32
+    # add (one block, ~1.2 us on the GPU) called back to back is bound by the
+    # calls, not the GPU; every kernel timed below runs longer than this, so
+    # its launches queue up ahead of the GPU
+    if wanted("host_call_floor_add_f32_64"):
+        def tiny():
+            return (filled("f32", (64,), "uniform", 0, 0, -1.0, 1.0),
+                    filled("f32", (64,), "uniform", 0, 1, -1.0, 1.0), T("f32", (64,)))
+        # one operand set (768 bytes: nothing to keep out of the cache)
+        batches, _ = timed(tiny, lambda s: sdk.call("tensor_add_f32", s[0], s[1], s[2]),
+                           ROTATE_BYTES)
+        results["host_call_floor_add_f32_64"] = {
+            "avg_us": round(min(batches) * 1e3, 2),
+            "batches_us": [round(b * 1e3, 2) for b in batches],
+            "note": "one-block kernel called back to back from Python: the host's per-call "
+                    "cost (the GPU side of the same launch is ~1.2 us)"}
     # cfg1: f32 add / mul / row-bias add [1024, 4096], U[-1,1], seed 0
     def cfg1():
         return (filled("f32", (1024, 4096), "uniform", 0, 0, -1.0, 1.0),
