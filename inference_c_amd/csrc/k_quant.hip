@@ -6,10 +6,11 @@
 // 16 bytes holding weight j in the low nibble and weight j+16 in the high
 // nibble of byte j, stored as value + 8 (Q4_0, 18 bytes).
 //
-// quant_gemv_kernel (1-4 input rows) and quant_mfma_kernel (5 or more):
+// quant_gemv_kernel (one input row) and quant_mma_kernel (two or more):
 // y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
-// A wave owns O output rows and walks them in chunks of 64 blocks. Each
-// chunk of each row is a contiguous byte range; the wave reads it with
+//
+// GEMV: a wave owns O output rows and walks them in chunks of 64 blocks.
+// Each chunk of each row is a contiguous byte range; the wave reads it with
 // coalesced 16-byte loads (the aligned 16-byte segments covering the range)
 // into its own LDS region, then lane l takes block l of the chunk from LDS:
 // blocks start on 2-byte boundaries, so the lane reads the 4-byte words
@@ -21,10 +22,11 @@
 // and multiplied with the x pairs by v_dot2_f32_f16, f32 accumulation; x for
 // the lane's block is loaded once per chunk and reused for all O rows. The
 // wave's partial sums are folded with DPP at the end. Bound: HBM bytes of
-// the packed weights (1.0625 or 0.5625 bytes per weight) at small row
-// counts.
+// the packed weights (1.0625 or 0.5625 bytes per weight).
 #include "kern_common.hpp"
 #include "kernels.hpp"
+
+#include <type_traits>
 
 namespace icsdk {
 namespace k {
@@ -37,6 +39,14 @@ template <bool kQ8> struct Fmt {
     static constexpr uint32_t kBytes = kQ8 ? 34 : 18;
     static constexpr int kWords = kQ8 ? 8 : 4;  // 4-byte words of packed values
 };
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled.
+template <int N, int I = 0, typename F> __device__ inline void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 __device__ inline half2_t as_half2(uint32_t bits) { return __builtin_bit_cast(half2_t, bits); }
 
@@ -212,148 +222,240 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         }
 }
 
-// quant_mfma_kernel (several input rows): a block owns 16 output rows o and
-// 16 * NR input rows r; its 4 waves split the weight blocks (k) in four and
-// fold their sums through LDS at the end. For each 32-weight block: B = the
-// 16 x 32 weight tile, transposed (lane l holds o = l % 16, k = 8 (l / 16)
-// .. +7), decoded exactly to f16; A_n = x rows 16 n + l % 16 at the same k;
-// one v_mfma_f32_16x16x32_f16 per n gives the block's dot products D[r][o]
-// (lane l holds r = 4 (l / 16) + i, o = l % 16), accumulated as acc =
-// fma(scale_o, D, acc) in f32 -- all of a lane's values share its o, so one
-// scale per lane and block. Each weight is decoded once for all 16 NR rows
-// (the GEMV decodes it once per row). W rows are staged through LDS in
-// chunks of 16 blocks, coalesced 16-byte loads as in the GEMV.
-template <bool kQ8, int NR>
-__global__ __launch_bounds__(kBlock) void quant_mfma_kernel(const uint16_t *__restrict__ x,
-                                                            const uint8_t *__restrict__ w,
-                                                            uint16_t *__restrict__ y,
-                                                            uint32_t rows, uint32_t in,
-                                                            uint32_t out) {
+// quant_mma_kernel (16 input rows per block row): each 32-weight block of 16
+// output rows o is one v_mfma_f32_16x16x32_f16 against the same block of 16
+// x rows r: B = the 16 x 32 weight tile, lane l holding o = l % 16 and 8 of
+// its k, decoded exactly to f16; A = the x rows at the same k; D[r][o] lands
+// in lane l as r = 4 (l / 16) + i, o = l % 16, so one scale per lane and
+// block. Each weight is decoded once for all 16 rows.
+//
+// Decode. A value byte u (Q8: the int8 XOR 0x80, i.e. q + 128; Q4: a nibble
+// shifted up by 4, i.e. 16 n) becomes the f16 bit pattern 0x00uu, the
+// subnormal u * 2^-24 -- one v_perm_b32 per two weights, no subtraction. The
+// products x * u * 2^-24 are exact in f32. The offset (Q8: 128; Q4: 16 * 8)
+// is removed by a second MFMA of the same x against a constant B of
+// -128 * 2^-24, accumulated onto the first, so
+//   D = 2^-24 * sum_k x_k q_k        (Q8)    D = 2^-20 * sum_k x_k (n_k - 8)   (Q4)
+// and acc = fma(scale, D, acc) with the f16 scale read straight into
+// v_fma_mix_f32. The result is multiplied by 2^24 (2^20) before rounding to
+// f16 (exact: a power of two). Per 32-weight block and lane: 8 (Q8) or 7
+// (Q4) VALU operations of decode, 4 FMAs, 2 MFMAs.
+//
+// k order. The MFMA sums over its 32 k in any order, so x and the weights
+// only have to agree: Q8 lane group g = lane / 16 takes weights 8g .. 8g+7
+// (value bytes 8g .. 8g+7); Q4 lane group g takes weights 4g .. 4g+3 (low
+// nibbles of value bytes 4g .. 4g+3) and 16+4g .. 16+4g+3 (their high
+// nibbles), so a Q4 lane reads one 4-byte word per block.
+//
+// Data movement. A block's 4 waves own 4 tiles of 16 output rows and walk
+// the same weight blocks (k) in chunks of 16, so the x rows of a chunk (up
+// to 16 rows x 1 KB) are loaded once per block -- contiguous 16-byte loads
+// into a double-buffered LDS chunk -- and every wave reads its MFMA operand
+// from there. (Each wave loading x in the MFMA layout itself moved 1 KB per
+// 512 weights through the address unit and bound the kernel.) Each wave
+// stages its 16 rows' next chunk of weights in registers with coalesced
+// 16-byte loads while it computes the current one from its LDS region.
+template <bool kQ8>
+__global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__restrict__ x,
+                                                           const uint8_t *__restrict__ w,
+                                                           uint16_t *__restrict__ y,
+                                                           uint32_t rows, uint32_t in,
+                                                           uint32_t out) {
     constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
-    constexpr uint32_t kWaves = kBlock / kWave;
-    constexpr uint32_t kChunkBlocks = 16;
-    constexpr uint32_t kVecs = kChunkBlocks * kBytes / 16 + 2;   // segments covering a row's chunk
-    constexpr uint32_t kSegs = 16 * kVecs;                       // per wave: 16 rows
+    constexpr uint32_t kWaves = kBlock / kWave;              // output tiles per block
+    constexpr uint32_t kChunk = 16;                          // weight blocks per chunk
+    constexpr uint32_t kChunkBytes = kChunk * kBytes;        // a multiple of 16
+    constexpr uint32_t kVecs = kChunkBytes / 16 + 2;         // segments covering a row's chunk
+    constexpr uint32_t kRowStride = (kVecs + 1) * 16;        // one spare segment per row: banks
+    constexpr uint32_t kSegs = 16 * kVecs;
     constexpr uint32_t kPasses = (kSegs + kWave - 1) / kWave;
-    constexpr uint32_t kStage = 16 * kVecs * 16;                 // bytes per wave
-    static_assert((size_t)kWaves * NR * kWave * 16 <= (size_t)kWaves * kStage, "fold fits the stage");
-    __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves * kStage];
+    constexpr uint32_t kStage = 16 * kRowStride;             // weight bytes per wave
+    constexpr uint32_t kXRow = kChunk * 64 + 16;             // an x row of a chunk (+ bank pad)
+    constexpr uint32_t kXBuf = 16 * kXRow;
+    constexpr uint32_t kXPasses = 16 / kWaves;               // x rows per wave and chunk
+    // chunks of registers in flight (2 and 3 measured no faster: the kernel
+    // is bound by issue and dependency stalls, not by memory latency)
+    constexpr int kDepth = 1;
+    static_assert(kChunkBytes % 16 == 0, "chunks start at one offset in their first segment");
+    static_assert(kChunk * 4 == kWave, "a lane stages one 16-byte x segment per row");
+    __shared__ __attribute__((aligned(16))) uint8_t wstage[kWaves * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[2 * kXBuf];
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t wv = threadIdx.x / kWave;
-    uint8_t *region = stage + wv * kStage;
-    const uint32_t o0 = blockIdx.x * 16;   // < out (the grid covers out exactly)
-    const uint32_t r0 = blockIdx.y * 16 * NR;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    uint8_t *region = wstage + wv * kStage;
+    // this wave's tile: rows o0 .. o0+15 (a tile past the end stages the
+    // last row and stores nothing; it still loads its share of x)
+    const uint32_t o0 = blockIdx.x * (16 * kWaves) + 16 * wv;
+    const uint32_t t0 = min(o0, out - 1);
+    const uint32_t last_row = min(15u, out - 1 - t0);
+    const uint32_t r0 = blockIdx.y * 16;
+    const uint32_t xrows = min(16u, rows - r0);
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
     const uint32_t col = lane % 16, grp = lane / 16;
-    // this wave's quarter of the weight blocks
-    const uint32_t per = (blocks + kWaves - 1) / kWaves;
-    const uint32_t kb0 = min(wv * per, blocks), kb1 = min(kb0 + per, blocks);
-    // rows past the end are clamped onto the last one (computed, not stored)
-    const uint8_t *my_row = w + (uint64_t)min(o0 + col, out - 1) * row_bytes;
-    const uint16_t *xrow[NR];
-#pragma unroll
-    for (int n = 0; n < NR; ++n) xrow[n] = x + (uint64_t)min(r0 + 16 * n + col, rows - 1) * in + 8 * grp;
-    f32x4 acc[NR];
-#pragma unroll
-    for (int n = 0; n < NR; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const half2_t bias8 = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
-    const half2_t bias4 = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
-    // Q4: lanes with k >= 16 take the high nibbles of bytes 8 (grp % 2) ..
-    const uint32_t nibble_shift = kQ8 ? 0u : (grp >= 2 ? 4u : 0u);
-    const uint32_t byte0 = 2 + 8 * (kQ8 ? grp : grp % 2);   // the lane's first value byte in a block
 
-    for (uint32_t c0 = kb0; c0 < kb1; c0 += kChunkBlocks) {
-        const uint32_t nb = min(kChunkBlocks, kb1 - c0);
-        // stage: wave segment v is segment v % kVecs of row v / kVecs's
-        // aligned cover; every lane loads (clamped), so no load sits behind
-        // a per-lane branch
-        u32x4 seg[kPasses];
+    // ---- weights: pass i, lane l loads segment v = l + 64 i of the tile's
+    // 16 row covers (row v / kVecs, segment v % kVecs); rows past the end
+    // are clamped onto the last one. A row's chunks all start `lead` bytes
+    // into their first segment; offsets are from tile + c0 * kBytes - 16 (so
+    // none is negative) and fit 32 bits (the launcher checks 16 rows do).
+    const uint8_t *tile = w + (uint64_t)t0 * row_bytes;
+    auto lead_of = [&](uint32_t row) -> uint32_t {
+        return (uint32_t)((reinterpret_cast<uintptr_t>(tile) + (uint64_t)row * row_bytes) & 15u);
+    };
+    // the offset of segment v of a chunk of nb blocks, clamped onto the
+    // chunk's last segment
+    auto seg_off = [&](uint32_t v, uint32_t nb) -> uint32_t {
+        const uint32_t row = min(min(v / kVecs, 15u), last_row), sidx = v % kVecs;
+        const uint32_t lead = lead_of(row);
+        const uint32_t last = (lead + nb * kBytes + 15) / 16 - 1;
+        return (uint32_t)(row * row_bytes) - lead + 16 + 16 * min(sidx, last);
+    };
+    uint32_t off_full[kPasses], lds_dst[kPasses];
 #pragma unroll
-        for (int i = 0; i < (int)kPasses; ++i) {
-            const uint32_t v = lane + kWave * i;
-            const uint32_t row = min(v / kVecs, 15u), sidx = v % kVecs;
-            const uint8_t *start = w + (uint64_t)min(o0 + row, out - 1) * row_bytes + (uint64_t)c0 * kBytes;
-            const uint32_t lead = (uint32_t)(reinterpret_cast<uintptr_t>(start) & 15u);
-            const uint32_t last = (lead + nb * kBytes + 15) / 16 - 1;
-            seg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(start - lead) + min(sidx, last));
-        }
-#pragma unroll
-        for (int i = 0; i < (int)kPasses; ++i) {
-            const uint32_t v = lane + kWave * i;
-            if (v < kSegs) *reinterpret_cast<u32x4 *>(region + (v / kVecs) * (kVecs * 16) + (v % kVecs) * 16) = seg[i];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint32_t my_lead =
-            (uint32_t)(reinterpret_cast<uintptr_t>(my_row + (uint64_t)c0 * kBytes) & 15u);
-        const uint8_t *mine = region + col * (kVecs * 16);
-        auto block = [&](uint32_t b) {
-            const uint32_t off = my_lead + b * kBytes;   // even: the block's scale
-            const uint32_t sword = *reinterpret_cast<const uint32_t *>(mine + (off & ~3u));
-            const float scale = (float)__builtin_bit_cast(
-                _Float16, (uint16_t)((off & 2u) ? sword >> 16 : sword & 0xffffu));
-            // the lane's 8 value bytes, re-aligned from the 3 words covering them
-            const uint32_t p = off + byte0;
-            const uint32_t *pw = reinterpret_cast<const uint32_t *>(mine + (p & ~3u));
-            const uint32_t e0 = pw[0], e1 = pw[1], e2 = pw[2];
-            const uint32_t sel = (p & 2u) ? 0x05040302u : 0x03020100u;
-            const uint32_t q[2] = {__builtin_amdgcn_perm(e1, e0, sel), __builtin_amdgcn_perm(e2, e1, sel)};
-            half8 bq;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                half2_t lo, hi;
-                if constexpr (kQ8) {
-                    const uint32_t u = q[j] ^ 0x80808080u;
-                    lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias8;
-                    hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias8;
-                } else {
-                    const uint32_t u = q[j] >> nibble_shift;
-                    lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u) & 0xff0fff0fu) - bias4;
-                    hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u) & 0xff0fff0fu) - bias4;
-                }
-                bq[4 * j] = lo[0];
-                bq[4 * j + 1] = lo[1];
-                bq[4 * j + 2] = hi[0];
-                bq[4 * j + 3] = hi[1];
-            }
-#pragma unroll
-            for (int n = 0; n < NR; ++n) {
-                const half8 ax = *reinterpret_cast<const half8 *>(xrow[n] + (uint64_t)(c0 + b) * 32);
-                const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bq, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[n][i] = __builtin_fmaf(scale, d[i], acc[n][i]);
-            }
-        };
-        if (nb == kChunkBlocks) {
-#pragma unroll
-            for (uint32_t b = 0; b < kChunkBlocks; ++b) block(b);
-        } else {
-            for (uint32_t b = 0; b < nb; ++b) block(b);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+    for (int i = 0; i < (int)kPasses; ++i) {
+        const uint32_t v = lane + kWave * i;
+        off_full[i] = seg_off(v, kChunk);
+        lds_dst[i] = min(v / kVecs, 15u) * kRowStride + (v % kVecs) * 16;
     }
-    // fold the 4 waves' sums: every wave reaches both barriers
-    __syncthreads();
-    f32x4 *fold = reinterpret_cast<f32x4 *>(stage);
+    u32x4 seg[kDepth][kPasses];
+    auto fetch_w = [&](u32x4 (&dst)[kPasses], uint32_t c0) {
+        const uint32_t nb = min(kChunk, blocks - c0);
+        const uint8_t *base = tile + (uint64_t)c0 * kBytes - 16;
+        if (nb == kChunk) {
 #pragma unroll
-    for (int n = 0; n < NR; ++n) fold[(wv * NR + n) * kWave + lane] = acc[n];
-    __syncthreads();
-    if (wv != 0) return;
-    const uint32_t o = o0 + col;
+            for (int i = 0; i < (int)kPasses; ++i)
+                dst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off_full[i]));
+        } else {
 #pragma unroll
-    for (int n = 0; n < NR; ++n) {
-        f32x4 t = fold[n * kWave + lane];
-#pragma unroll
-        for (uint32_t u = 1; u < kWaves; ++u) t += fold[(u * NR + n) * kWave + lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = r0 + 16 * n + 4 * grp + i;
-            if (r < rows && o < out)
-                y[(uint64_t)r * out + o] = __builtin_bit_cast(uint16_t, (_Float16)t[i]);
+            for (int i = 0; i < (int)kPasses; ++i)
+                dst[i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(base + seg_off(lane + kWave * i, nb)));
         }
+    };
+
+    // ---- x: wave wv stages rows wv, wv + 4, .. of the chunk (lane l: bytes
+    // 16 l .. 16 l + 15 of the row's 1 KB; past a partial chunk's end the
+    // last segment again)
+    const uint16_t *x_tile = x + (uint64_t)r0 * in;
+    u32x4 xseg[kDepth][kXPasses];
+    auto fetch_x = [&](u32x4 (&dst)[kXPasses], uint32_t c0) {
+        const uint32_t nb = min(kChunk, blocks - c0);
+        const uint32_t sg = min(lane, nb * 4 - 1);
+#pragma unroll
+        for (int i = 0; i < (int)kXPasses; ++i) {
+            const uint32_t xr = wv + kWaves * i;
+            if (xr < xrows)
+                dst[i] = *reinterpret_cast<const u32x4 *>(x_tile + (uint64_t)xr * in +
+                                                          (uint64_t)c0 * 32 + sg * 8);
+        }
+    };
+
+    // ---- this lane's reads: weights of row `col` -- value bytes of block b
+    // start at a0 + kBytes * b; a block's word-aligned cover starts at
+    // f_even + kBytes * b for even b, f_odd + kBytes * (b - 1) for odd b
+    // (kBytes is 2 mod 4, so the alignment alternates, and the re-aligning
+    // selector with it); x of row min(col, xrows - 1)
+    const uint32_t my_lead = lead_of(min(col, last_row));
+    const uint32_t koff = kQ8 ? 8 * grp : 4 * grp;
+    const uint32_t row_base = col * kRowStride;
+    const uint32_t a0 = row_base + my_lead + 2 + koff;
+    const uint32_t f_even = a0 & ~3u;
+    const uint32_t f_odd = (a0 & 2u) ? f_even + 2 + kBytes : f_even - 2 + kBytes;
+    const uint32_t sel_even = (a0 & 2u) ? 0x05040302u : 0x03020100u;
+    const uint32_t sel_odd = (a0 & 2u) ? 0x03020100u : 0x05040302u;
+    const uint32_t scale_base = row_base + my_lead;
+    const uint32_t x_base = min(col, xrows - 1) * kXRow + 2 * koff;
+
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const half8 offset_b = __builtin_bit_cast(half8, u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u});
+    // chunks c+1 .. c+kDepth-1 are in flight while chunk c is computed;
+    // chunk c's registers are slot c % kDepth (the loop is unrolled by
+    // kDepth so the slot is static)
+#pragma unroll
+    for (int p = 0; p < kDepth; ++p)
+        if ((uint32_t)p * kChunk < blocks) {
+            fetch_w(seg[p], p * kChunk);
+            fetch_x(xseg[p], p * kChunk);
+        }
+    auto step = [&](auto pc, uint32_t c0) {
+        constexpr int p = decltype(pc)::value;
+        const uint32_t nb = min(kChunk, blocks - c0);
+        uint8_t *xbuf = xstage + ((c0 / kChunk) & 1u) * kXBuf;
+#pragma unroll
+        for (int i = 0; i < (int)kPasses; ++i)
+            if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[p][i];
+#pragma unroll
+        for (int i = 0; i < (int)kXPasses; ++i) {
+            const uint32_t xr = wv + kWaves * i;
+            if (xr < xrows) *reinterpret_cast<u32x4 *>(xbuf + xr * kXRow + lane * 16) = xseg[p][i];
+        }
+        // every wave's x rows and this wave's weights are in LDS; every wave
+        // is past the chunk before the last, which read the other x buffer
+        __syncthreads();
+        if (c0 + kDepth * kChunk < blocks) {
+            fetch_w(seg[p], c0 + kDepth * kChunk);
+            fetch_x(xseg[p], c0 + kDepth * kChunk);
+        }
+        auto block = [&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const uint32_t cover = (j % 2 == 0 ? f_even : f_odd) + kBytes * (j & ~1);
+            const uint32_t sel = j % 2 == 0 ? sel_even : sel_odd;
+            const uint32_t *pw = reinterpret_cast<const uint32_t *>(region + cover);
+            const uint16_t sbits = *reinterpret_cast<const uint16_t *>(region + scale_base + kBytes * j);
+            const uint8_t *xa = xbuf + x_base + 64 * j;
+            u32x4 bw, aw;
+            if constexpr (kQ8) {
+                const uint32_t e0 = pw[0], e1 = pw[1], e2 = pw[2];
+                const uint32_t u0 = __builtin_amdgcn_perm(e1, e0, sel) ^ 0x80808080u;
+                const uint32_t u1 = __builtin_amdgcn_perm(e2, e1, sel) ^ 0x80808080u;
+                bw = u32x4{__builtin_amdgcn_perm(0u, u0, 0x0c010c00u), __builtin_amdgcn_perm(0u, u0, 0x0c030c02u),
+                           __builtin_amdgcn_perm(0u, u1, 0x0c010c00u), __builtin_amdgcn_perm(0u, u1, 0x0c030c02u)};
+                aw = *reinterpret_cast<const u32x4 *>(xa);
+            } else {
+                const uint32_t e0 = pw[0], e1 = pw[1];
+                const uint32_t q = __builtin_amdgcn_perm(e1, e0, sel);
+                const uint32_t hi = q & 0xf0f0f0f0u;
+                const uint32_t lo = (q << 4) & 0xf0f0f0f0u;
+                bw = u32x4{__builtin_amdgcn_perm(hi, lo, 0x0c010c00u), __builtin_amdgcn_perm(hi, lo, 0x0c030c02u),
+                           __builtin_amdgcn_perm(hi, lo, 0x0c050c04u), __builtin_amdgcn_perm(hi, lo, 0x0c070c06u)};
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 lo_x = *reinterpret_cast<const u32x2 *>(xa);
+                const u32x2 hi_x = *reinterpret_cast<const u32x2 *>(xa + 32);
+                aw = u32x4{lo_x.x, lo_x.y, hi_x.x, hi_x.y};
+            }
+            const float scale = (float)__builtin_bit_cast(_Float16, sbits);
+            const half8 ax = __builtin_bit_cast(half8, aw);
+            f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, __builtin_bit_cast(half8, bw),
+                                                            f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, offset_b, d, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(scale, d[i], acc[i]);
+        };
+        if (nb == kChunk) {
+            static_for<kChunk>([&](auto jc) { block(jc); });
+        } else {
+            static_for<kChunk>([&](auto jc) {
+                if ((uint32_t)decltype(jc)::value < nb) block(jc);
+            });
+        }
+        // this wave's region is rewritten next: its reads come first
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    };
+    for (uint32_t c0 = 0; c0 < blocks; c0 += kDepth * kChunk)
+        static_for<kDepth>([&](auto pc) {
+            const uint32_t c = c0 + decltype(pc)::value * kChunk;
+            if (c < blocks) step(pc, c);
+        });
+    if (o0 >= out) return;
+    const uint32_t o = o0 + col;
+    const float unit = kQ8 ? 16777216.0f : 1048576.0f;   // 2^24, 2^20
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = r0 + 4 * grp + i;
+        if (r < rows && o < out)
+            y[(uint64_t)r * out + o] = __builtin_bit_cast(uint16_t, (_Float16)(acc[i] * unit));
     }
 }
 
@@ -479,13 +581,13 @@ hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t 
     return hipGetLastError();
 }
 
-template <bool kQ8, int NR>
-hipError_t launch_mfma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows, size_t in,
-                       size_t out, hipStream_t s) {
-    if ((out + 15) / 16 > 0x7fffffffu) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((out + 15) / 16), (unsigned)((rows + 16 * NR - 1) / (16 * NR)));
-    quant_mfma_kernel<kQ8, NR><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                       (uint32_t)out);
+template <bool kQ8>
+hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows, size_t in,
+                      size_t out, hipStream_t s) {
+    constexpr size_t kRowsPerBlock = 16 * (kBlock / kWave);
+    const dim3 grid((unsigned)((out + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)((rows + 15) / 16));
+    quant_mma_kernel<kQ8><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                  (uint32_t)out);
     return hipGetLastError();
 }
 
@@ -504,33 +606,25 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
                                                                               (uint32_t)out);
         return hipGetLastError();
     }
-    // row groups per launch stay within the grid's y limit
+    // One input row: the GEMV (no x reuse to exploit; its dot products cost
+    // no more VALU per weight than the MFMA decode and it needs no x staging).
+    // Two or more: quant_mma_kernel decodes each weight once for up to 16
+    // rows ([28672, 8192] Q8_0, 16 rows: 82 -> 55 us over a 16-row MFMA
+    // kernel that loaded x per wave; 4 rows 66 -> 52 us over a 4-row GEMV).
+    // Its 32-bit offsets bound `in`; past that every row takes the GEMV.
+    // Row groups per launch stay within the grid's y limit.
     constexpr size_t kMaxGroups = 65535;
+    const bool mma = rows >= 2 && in <= (size_t{1} << 25);
     for (size_t r0 = 0; r0 < rows;) {
         const size_t left = rows - r0;
-        const uint16_t *xr = x + r0 * in;
-        uint16_t *yr = y + r0 * out;
         hipError_t status;
         size_t done;
-        // up to 4 rows the GEMV (one dot per weight and row) is faster; from
-        // 5 rows the MFMA kernel, which decodes each weight once for 16 or
-        // 32 rows (8 rows of 8192 -> 28672: 98 -> 71 us for Q8, 16 rows 188
-        // -> 84 us)
-        if (left <= 1) {
-            status = launch_gemv<kQ8, 1, kQ8 ? 4 : 2>(xr, w, yr, left, in, out, s);
-            done = left;
-        } else if (left <= 2) {
-            status = launch_gemv<kQ8, 2, 4>(xr, w, yr, left, in, out, s);
-            done = left;
-        } else if (left <= 4) {
-            status = launch_gemv<kQ8, 4, 4>(xr, w, yr, left, in, out, s);
-            done = left;
-        } else if (left <= 16) {
-            status = launch_mfma<kQ8, 1>(xr, w, yr, left, in, out, s);
-            done = left;
+        if (mma) {
+            done = left < kMaxGroups * 16 ? left : kMaxGroups * 16;
+            status = launch_mma<kQ8>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else {
-            done = left < kMaxGroups * 32 ? left : kMaxGroups * 32;
-            status = launch_mfma<kQ8, 2>(xr, w, yr, done, in, out, s);
+            done = left < kMaxGroups ? left : kMaxGroups;
+            status = launch_gemv<kQ8, 1, kQ8 ? 4 : 2>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;

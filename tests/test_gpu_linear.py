@@ -296,7 +296,10 @@ def test_quantize_known_bytes(sdk):
 QUANT_SHAPES = [  # rows, in, out
     (1, 32, 1), (1, 64, 7), (1, 2048, 256), (2, 4096, 130), (3, 96, 33), (4, 1024, 64),
     (5, 512, 40), (8, 256, 16), (17, 2080, 24), (64, 768, 96), (1, 8192, 512),
-    (6, 8192, 100), (33, 544, 50),   # MFMA path: ragged outputs; a partial 32-row group, short key quarters
+    (6, 8192, 100), (33, 544, 50),
+    # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
+    # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
+    (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
 ]
 
 
