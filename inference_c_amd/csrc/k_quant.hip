@@ -14,13 +14,12 @@
 // coalesced 16-byte loads (the aligned 16-byte segments covering the range)
 // into its own LDS region, then lane l takes block l of the chunk from LDS:
 // blocks start on 2-byte boundaries, so the lane reads the 4-byte words
-// covering its block and re-aligns them with v_perm_b32. (Loading each
-// lane's block straight from memory -- 34 bytes at a 34-byte lane stride --
-// spreads every load instruction over ~17 cache lines and ran at half the
-// rate.) The int8 / nibble values are turned into exact f16 pairs
-// (0x6400 | byte is 1024 + byte; one packed f16 subtract removes the offset)
-// and multiplied with the x pairs by v_dot2_f32_f16, f32 accumulation; x for
-// the lane's block is loaded once per chunk and reused for all O rows. The
+// covering its block. (Loading each lane's block straight from memory -- 34
+// bytes at a 34-byte lane stride -- spreads every load instruction over ~17
+// cache lines and ran at half the rate.) One v_perm_b32 per value-byte pair
+// both re-aligns it and turns it into two exact f16 subnormals, multiplied
+// with the x pairs by v_dot2_f32_f16 in f32 (gemv_block below); x for the
+// lane's block is loaded once per chunk and reused for all O rows. The
 // wave's partial sums are folded with DPP at the end. Bound: HBM bytes of
 // the packed weights (1.0625 or 0.5625 bytes per weight).
 #include "kern_common.hpp"
@@ -37,7 +36,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 template <bool kQ8> struct Fmt {
     static constexpr uint32_t kBytes = kQ8 ? 34 : 18;
-    static constexpr int kWords = kQ8 ? 8 : 4;  // 4-byte words of packed values
 };
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled.
@@ -50,75 +48,73 @@ template <int N, int I = 0, typename F> __device__ inline void static_for(F &&f)
 
 __device__ inline half2_t as_half2(uint32_t bits) { return __builtin_bit_cast(half2_t, bits); }
 
-// Reads the block at byte offset `off` (even) of an LDS chunk: its scale
-// and its packed values re-aligned to 4-byte words. The reads cover the
-// block and at most the 2 bytes before it; both tail reads are
-// unconditional (an aligned block reads its last half-word twice and uses
-// only the low half).
+// GEMV block arithmetic. Lane l of a chunk owns block l; the block starts at
+// an even byte offset `off` of the staged row, so the kWin 4-byte words read
+// from off & ~3 hold it (with at most 2 bytes either side): its value byte k
+// sits at window byte 2 + k + sh, sh = off & 2, and its scale at bytes sh,
+// sh + 1. Value-byte pair j (bytes 2j, 2j + 1) lies in one word -- word
+// pair (w_m, w_m+1) holds pair 2m at bytes 2 + sh, 3 + sh and pair 2m + 1 at
+// 4 + sh, 5 + sh -- so one v_perm_b32 with a per-lane selector re-aligns it
+// and spreads it into the low bytes of two halves at once: 0x00bb00aa, two
+// f16 subnormals a * 2^-24, b * 2^-24. Their products with x are exact in
+// f32 (v_dot2_f32_f16); the constant part of the value encoding is removed
+// once per block through the block's x sum X (shared by the wave's rows):
+//   Q8: byte ^ 0x80 = q + 128      sum x q = 2^24 S - 128 X
+//   Q4: nibble n = w + 8 (low nibbles masked in place, high nibbles as 16 n)
+//                                  sum x w = 2^24 (S + H / 16) - 8 X
+template <bool kQ8> struct GemvFmt {
+    static constexpr int kWin = kQ8 ? 9 : 5;
+};
+
+struct GemvSel {
+    uint32_t a, b, s;   // value pairs 2m and 2m + 1 of (w_m, w_m+1); the scale of w_0
+    GemvSel() = default;
+    __device__ explicit GemvSel(uint32_t sh)
+        : a(sh ? 0x0c050c04u : 0x0c030c02u), b(sh ? 0x0c070c06u : 0x0c050c04u),
+          s(sh ? 0x0c0c0302u : 0x0c0c0100u) {}
+};
+
+// sum_k x_k w_k of one block (f32) and its scale; x holds the block's 32 f16
+// as 16 pairs, xsum their sum.
 template <bool kQ8>
-__device__ inline float read_block(const uint8_t *chunk, uint32_t off,
-                                   uint32_t (&q)[Fmt<kQ8>::kWords]) {
-    constexpr int W = Fmt<kQ8>::kWords;
-    const uint32_t shift = off & 2u;
-    const uint8_t *base = chunk + (off - shift);
-    const uint32_t *words = reinterpret_cast<const uint32_t *>(base);
-    uint32_t e[W + 1];
+__device__ inline float gemv_block(const uint8_t *chunk, uint32_t off, const GemvSel &sel,
+                                   const uint32_t (&x)[16], float xsum, float &scale) {
+    constexpr int W = GemvFmt<kQ8>::kWin;
+    const uint32_t *words = reinterpret_cast<const uint32_t *>(chunk + (off & ~3u));
+    uint32_t e[W];
 #pragma unroll
     for (int i = 0; i < W; ++i) e[i] = words[i];
-    const uint16_t *tail = reinterpret_cast<const uint16_t *>(base + 4 * W);
-    e[W] = (uint32_t)tail[0] | (uint32_t)tail[shift >> 1] << 16;
-    const uint32_t sel = shift ? 0x07060504u : 0x05040302u;
-#pragma unroll
-    for (int i = 0; i < W; ++i) q[i] = __builtin_amdgcn_perm(e[i + 1], e[i], sel);
-    const uint32_t scale_bits = shift ? (e[0] >> 16) : (e[0] & 0xffffu);
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)scale_bits);
-}
-
-// sum_k x_k q_k of one block in f32; x holds the block's 32 f16 as 16 pairs.
-template <bool kQ8>
-__device__ inline float block_dot(const uint32_t (&q)[Fmt<kQ8>::kWords], const uint32_t (&x)[16]) {
-    const half2_t bias8 = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
-    const half2_t bias4 = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
+    scale = (float)__builtin_bit_cast(_Float16, (uint16_t)__builtin_amdgcn_perm(e[0], e[0], sel.s));
     float s0 = 0.0f, s1 = 0.0f;
     if constexpr (kQ8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // int8 -> offset binary, two bytes per f16 pair
-            const uint32_t u = q[j] ^ 0x80808080u;
-            const half2_t lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias8;
-            const half2_t hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias8;
-            s0 = __builtin_amdgcn_fdot2(lo, as_half2(x[2 * j]), s0, false);
-            s1 = __builtin_amdgcn_fdot2(hi, as_half2(x[2 * j + 1]), s1, false);
+        for (int i = 0; i < W; ++i) e[i] ^= 0x80808080u;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            s0 = __builtin_amdgcn_fdot2(as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.a)),
+                                        as_half2(x[2 * m]), s0, false);
+            s1 = __builtin_amdgcn_fdot2(as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.b)),
+                                        as_half2(x[2 * m + 1]), s1, false);
         }
+        return __builtin_fmaf(s0 + s1, 16777216.0f, -128.0f * xsum);
     } else {
-        // byte b of the word into the low byte of a half with 0x64 above it:
-        // 0x64bb = 1024 + lo + 16 hi. Masking keeps 1024 + lo (0x640n) or
-        // 1024 + 16 hi (0x64n0); the packed subtract leaves lo - 8 and
-        // 16 (hi - 8), both exact in f16. The high-nibble products go to
-        // their own sums, scaled by 1/16 (exact) at the end.
-        const half2_t bias16 = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 16 * 8
         float h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, q[j], 0x04010400u);
-            const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, q[j], 0x04030402u);
-            const half2_t w01 = as_half2(p01 & 0xff0fff0fu) - bias4;
-            const half2_t w23 = as_half2(p23 & 0xff0fff0fu) - bias4;
-            const half2_t w1617 = as_half2(p01 & 0xfff0fff0u) - bias16;
-            const half2_t w1819 = as_half2(p23 & 0xfff0fff0u) - bias16;
-            s0 = __builtin_amdgcn_fdot2(w01, as_half2(x[2 * j]), s0, false);
-            s1 = __builtin_amdgcn_fdot2(w23, as_half2(x[2 * j + 1]), s1, false);
-            h0 = __builtin_amdgcn_fdot2(w1617, as_half2(x[8 + 2 * j]), h0, false);
-            h1 = __builtin_amdgcn_fdot2(w1819, as_half2(x[8 + 2 * j + 1]), h1, false);
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t pa = __builtin_amdgcn_perm(e[m + 1], e[m], sel.a);
+            const uint32_t pb = __builtin_amdgcn_perm(e[m + 1], e[m], sel.b);
+            s0 = __builtin_amdgcn_fdot2(as_half2(pa & 0x000f000fu), as_half2(x[2 * m]), s0, false);
+            s1 = __builtin_amdgcn_fdot2(as_half2(pb & 0x000f000fu), as_half2(x[2 * m + 1]), s1, false);
+            h0 = __builtin_amdgcn_fdot2(as_half2(pa & 0x00f000f0u), as_half2(x[8 + 2 * m]), h0, false);
+            h1 = __builtin_amdgcn_fdot2(as_half2(pb & 0x00f000f0u), as_half2(x[8 + 2 * m + 1]), h1, false);
         }
-        return (s0 + s1) + (h0 + h1) * 0.0625f;
+        return __builtin_fmaf(__builtin_fmaf(h0 + h1, 0.0625f, s0 + s1), 16777216.0f, -8.0f * xsum);
     }
-    return s0 + s1;
 }
 
-// Grid: x = waves of O output rows (4 waves per block), y = groups of R input
-// rows. Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
-template <bool kQ8, int R, int O>
+// Grid: x = waves of O output rows (4 waves per block), y = input rows.
+// Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
+template <bool kQ8, int O>
 __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
                                                             uint16_t *__restrict__ y,
@@ -127,7 +123,6 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
     constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
     constexpr uint32_t kChunk = kWave * kBytes;        // bytes of 64 blocks
     constexpr uint32_t kVecs = kChunk / 16 + 2;        // 16-byte segments covering a chunk
-    constexpr uint32_t kPasses = (kVecs + kWave - 1) / kWave;
     __shared__ __attribute__((aligned(16))) uint8_t stage[kBlock / kWave][O][kVecs * 16];
     const uint32_t lane = threadIdx.x & (kWave - 1);
     uint8_t (*region)[kVecs * 16] = stage[threadIdx.x / kWave];
@@ -135,63 +130,81 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         (blockIdx.x * kBlock + threadIdx.x) / kWave);
     const uint32_t o0 = wave * O;
     if (o0 >= out) return;
-    const uint32_t r0 = blockIdx.y * R;
+    const uint32_t r = blockIdx.y;
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
-    // rows past the end are clamped onto the last one (computed, not stored)
-    const uint8_t *wrow[O];
-    const uint16_t *xrow[R];
+    const uint16_t *xrow = x + (uint64_t)r * in;
+    // rows past the end are clamped onto the last one (computed, not stored).
+    // A chunk of 64 blocks is a whole number of 16-byte segments, so every
+    // chunk of a row starts `lead` bytes into its first segment, and lane
+    // l's block starts at lead + kBytes * l: its alignment (and selectors)
+    // are the same in every chunk.
+    auto row_of = [&](uint32_t o) -> uint64_t { return (uint64_t)min(o0 + o, out - 1); };
+    auto lead_of = [&](uint64_t row) -> uint32_t {
+        return (uint32_t)((reinterpret_cast<uintptr_t>(w) + row * row_bytes) & 15u);
+    };
+    uint32_t lead[O];
 #pragma unroll
-    for (int o = 0; o < O; ++o) wrow[o] = w + (uint64_t)min(o0 + o, out - 1) * row_bytes;
-#pragma unroll
-    for (int r = 0; r < R; ++r) xrow[r] = x + (uint64_t)min(r0 + r, rows - 1) * in;
+    for (int o = 0; o < O; ++o) lead[o] = lead_of(row_of(o));
+    const uint8_t *tile = w + row_of(0) * row_bytes;
+    // lane l's selectors: its block's alignment is the row's lead parity
+    // flipped on odd lanes (kBytes is 2 mod 4), so two sets serve every row.
+    // (A lane past a partial chunk's end reads block nb - 1 with them:
+    // garbage, discarded.)
+    const GemvSel sel_lead0((kBytes * lane) & 2u), sel_lead2((2 + kBytes * lane) & 2u);
 
-    float acc[O][R];
+    float acc[O];
 #pragma unroll
-    for (int o = 0; o < O; ++o)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[o][r] = 0.0f;
+    for (int o = 0; o < O; ++o) acc[o] = 0.0f;
 
     for (uint32_t c0 = 0; c0 < blocks; c0 += kWave) {
         const uint32_t nb = min((uint32_t)kWave, blocks - c0);
         // the aligned 16-byte segments holding this chunk of each row; a
         // segment never crosses a page, so the bytes around the chunk that
-        // share its first and last segment are safe to read
-        uint32_t lead[O];
-        u32x4 seg[O][kPasses];
+        // share its first and last segment are safe to read. Lanes past the
+        // chunk's last segment load nothing (inactive lanes cost the address
+        // unit nothing; loading the last segment again in them measured
+        // 8% slower for Q8).
+        constexpr uint32_t kRowPasses = (kVecs + kWave - 1) / kWave;
+        u32x4 segr[O][kRowPasses];
 #pragma unroll
         for (int o = 0; o < O; ++o) {
-            const uint8_t *start = wrow[o] + (uint64_t)c0 * kBytes;
-            lead[o] = (uint32_t)(reinterpret_cast<uintptr_t>(start) & 15u);
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(start - lead[o]);
+            const uint8_t *src = tile + (row_of(o) - row_of(0)) * row_bytes + (uint64_t)c0 * kBytes - lead[o];
             const uint32_t nvec = (lead[o] + nb * kBytes + 15) / 16;
 #pragma unroll
-            for (int i = 0; i < (int)kPasses; ++i) {
+            for (int i = 0; i < (int)kRowPasses; ++i) {
                 const uint32_t v = lane + kWave * i;
-                seg[o][i] = v < nvec ? __builtin_nontemporal_load(src + v) : u32x4{0, 0, 0, 0};
+                segr[o][i] = v < nvec ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + v)
+                                      : u32x4{0, 0, 0, 0};
             }
         }
         const uint32_t b = c0 + min(lane, nb - 1);
-        uint32_t xv[R][16];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow[r] + (uint64_t)b * 32);
+        uint32_t xv[16];
+        {
+            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + (uint64_t)b * 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const u32x4 t = xp[v];
-                xv[r][4 * v] = t.x;
-                xv[r][4 * v + 1] = t.y;
-                xv[r][4 * v + 2] = t.z;
-                xv[r][4 * v + 3] = t.w;
+                xv[4 * v] = t.x;
+                xv[4 * v + 1] = t.y;
+                xv[4 * v + 2] = t.z;
+                xv[4 * v + 3] = t.w;
             }
         }
+        const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+        float xs0 = 0.0f, xs1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            xs0 = __builtin_amdgcn_fdot2(as_half2(xv[i]), one2, xs0, false);
+            xs1 = __builtin_amdgcn_fdot2(as_half2(xv[i + 1]), one2, xs1, false);
+        }
+        const float xsum = xs0 + xs1;
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
-            for (int i = 0; i < (int)kPasses; ++i) {
-                const uint32_t v = lane + kWave * i;
-                if (v < kVecs) *reinterpret_cast<u32x4 *>(&region[o][v * 16]) = seg[o][i];
-            }
+            for (int i = 0; i < (int)kRowPasses; ++i)
+                if (lane + kWave * i < kVecs)
+                    *reinterpret_cast<u32x4 *>(&region[o][(lane + kWave * i) * 16]) = segr[o][i];
         // the region is this wave's alone: order its LDS writes before the
         // reads of other lanes, and the reads before the next chunk's writes
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -200,26 +213,23 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         const bool live = lane < nb;
 #pragma unroll
         for (int o = 0; o < O; ++o) {
-            uint32_t q[Fmt<kQ8>::kWords];
-            const float scale = read_block<kQ8>(region[o], lead[o] + (b - c0) * kBytes, q);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float part = scale * block_dot<kQ8>(q, xv[r]);
-                acc[o][r] += live ? part : 0.0f;
-            }
+            const uint32_t off = lead[o] + (b - c0) * kBytes;
+            float scale;
+            const float dot = gemv_block<kQ8>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0,
+                                              xv, xsum, scale);
+            // a lane past the chunk's end adds 0 * (a finite dot): its scale
+            // bytes may be anything, its decoded values are subnormals
+            acc[o] = __builtin_fmaf(live ? scale : 0.0f, dot, acc[o]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (int o = 0; o < O; ++o)
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float total = wave_sum(acc[o][r]);
-            if (lane == 0 && o0 + o < out && r0 + r < rows)
-                y[(uint64_t)(r0 + r) * out + o0 + o] =
-                    __builtin_bit_cast(uint16_t, (_Float16)total);
-        }
+    for (int o = 0; o < O; ++o) {
+        const float total = wave_sum(acc[o]);
+        if (lane == 0 && o0 + o < out)
+            y[(uint64_t)r * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+    }
 }
 
 // quant_mma_kernel (16 input rows per block row): each 32-weight block of 16
@@ -569,15 +579,14 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const uint16_t *__rest
     }
 }
 
-template <bool kQ8, int R, int O>
+template <bool kQ8, int O>
 hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
                        size_t in, size_t out, hipStream_t s) {
     constexpr uint32_t kWavesPerBlock = kBlock / kWave;
     const size_t waves = (out + O - 1) / O;
-    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock),
-                    (unsigned)((rows + R - 1) / R));
-    quant_gemv_kernel<kQ8, R, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                         (uint32_t)out);
+    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock), (unsigned)rows);
+    quant_gemv_kernel<kQ8, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                      (uint32_t)out);
     return hipGetLastError();
 }
 
@@ -606,13 +615,14 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
                                                                               (uint32_t)out);
         return hipGetLastError();
     }
-    // One input row: the GEMV (no x reuse to exploit; its dot products cost
-    // no more VALU per weight than the MFMA decode and it needs no x staging).
-    // Two or more: quant_mma_kernel decodes each weight once for up to 16
-    // rows ([28672, 8192] Q8_0, 16 rows: 82 -> 55 us over a 16-row MFMA
-    // kernel that loaded x per wave; 4 rows 66 -> 52 us over a 4-row GEMV).
-    // Its 32-bit offsets bound `in`; past that every row takes the GEMV.
-    // Row groups per launch stay within the grid's y limit.
+    // One input row: the GEMV, 4 output rows per wave (2, 6 and 8 measured
+    // slower for both formats); it has no x reuse to exploit, its dot
+    // products cost no more VALU per weight than the MFMA decode and it needs
+    // no x staging. Two or more: quant_mma_kernel decodes each weight once
+    // for up to 16 rows ([28672, 8192] Q8_0, 16 rows: 82 -> 58 us over a
+    // 16-row MFMA kernel that loaded x per wave; 4 rows 66 -> 49 us over a
+    // 4-row GEMV). Its 32-bit offsets bound `in`; past that every row takes
+    // the GEMV. Row groups per launch stay within the grid's y limit.
     constexpr size_t kMaxGroups = 65535;
     const bool mma = rows >= 2 && in <= (size_t{1} << 25);
     for (size_t r0 = 0; r0 < rows;) {
@@ -624,7 +634,7 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
             status = launch_mma<kQ8>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else {
             done = left < kMaxGroups ? left : kMaxGroups;
-            status = launch_gemv<kQ8, 1, kQ8 ? 4 : 2>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+            status = launch_gemv<kQ8, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;
