@@ -265,6 +265,11 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 // 512 weights through the address unit and bound the kernel.) Each wave
 // stages its 16 rows' next chunk of weights in registers with coalesced
 // 16-byte loads while it computes the current one from its LDS region.
+// Measured limits ([28672, 8192] Q8_0, 4 and 16 rows): the loads, staging
+// and barriers alone take 44-50 us, the decode and MFMAs alone ~40 us
+// (about 2 waves per SIMD: 448 blocks, and a k split per block does not fit
+// in LDS); prefetching 2 or 3 chunks ahead, or issuing the offset MFMA
+// first, measured no faster.
 template <bool kQ8>
 __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__restrict__ x,
                                                            const uint8_t *__restrict__ w,
@@ -272,30 +277,32 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
                                                            uint32_t rows, uint32_t in,
                                                            uint32_t out) {
     constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
-    constexpr uint32_t kWaves = kBlock / kWave;              // output tiles per block
-    constexpr uint32_t kChunk = 16;                          // weight blocks per chunk
-    constexpr uint32_t kChunkBytes = kChunk * kBytes;        // a multiple of 16
-    constexpr uint32_t kVecs = kChunkBytes / 16 + 2;         // segments covering a row's chunk
-    constexpr uint32_t kRowStride = (kVecs + 1) * 16;        // one spare segment per row: banks
+    constexpr uint32_t kTiles = kBlock / kWave;               // output tiles per block
+    // weight blocks per chunk: a row's chunk is 544 (Q8) or 288 bytes
+    // contiguous. 8 blocks ran ~45% slower (shorter runs per row at the
+    // memory); 32 do not fit twice per CU in LDS.
+    constexpr uint32_t kChunk = 16;
+    constexpr uint32_t kChunkBytes = kChunk * kBytes;         // a multiple of 16
+    constexpr uint32_t kVecs = kChunkBytes / 16 + 2;          // segments covering a row's chunk
+    constexpr uint32_t kRowStride = (kVecs + 1) * 16;         // one spare segment per row: banks
     constexpr uint32_t kSegs = 16 * kVecs;
     constexpr uint32_t kPasses = (kSegs + kWave - 1) / kWave;
-    constexpr uint32_t kStage = 16 * kRowStride;             // weight bytes per wave
-    constexpr uint32_t kXRow = kChunk * 64 + 16;             // an x row of a chunk (+ bank pad)
+    constexpr uint32_t kStage = 16 * kRowStride;              // weight bytes per wave
+    constexpr uint32_t kXSegs = kChunk * 4;                   // 16-byte segments of an x row's chunk
+    constexpr uint32_t kXRow = kXSegs * 16 + 16;              // (+ bank pad)
     constexpr uint32_t kXBuf = 16 * kXRow;
-    constexpr uint32_t kXPasses = 16 / kWaves;               // x rows per wave and chunk
-    // chunks of registers in flight (2 and 3 measured no faster: the kernel
-    // is bound by issue and dependency stalls, not by memory latency)
-    constexpr int kDepth = 1;
+    constexpr uint32_t kXPasses = 16 * kXSegs / kBlock;       // x segments per thread
     static_assert(kChunkBytes % 16 == 0, "chunks start at one offset in their first segment");
-    static_assert(kChunk * 4 == kWave, "a lane stages one 16-byte x segment per row");
-    __shared__ __attribute__((aligned(16))) uint8_t wstage[kWaves * kStage];
-    __shared__ __attribute__((aligned(16))) uint8_t xstage[2 * kXBuf];
+    static_assert(16 * kXSegs % kBlock == 0, "x chunks split evenly over the threads");
+    __shared__ __attribute__((aligned(16))) uint8_t wstage[kTiles * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[2][kXBuf];
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    uint8_t *region = wstage + wv * kStage;
+    const uint32_t tile_i = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t pt = threadIdx.x;
+    uint8_t *region = wstage + tile_i * kStage;
     // this wave's tile: rows o0 .. o0+15 (a tile past the end stages the
     // last row and stores nothing; it still loads its share of x)
-    const uint32_t o0 = blockIdx.x * (16 * kWaves) + 16 * wv;
+    const uint32_t o0 = blockIdx.x * (16 * kTiles) + 16 * tile_i;
     const uint32_t t0 = min(o0, out - 1);
     const uint32_t last_row = min(15u, out - 1 - t0);
     const uint32_t r0 = blockIdx.y * 16;
@@ -303,12 +310,16 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
     const uint32_t col = lane % 16, grp = lane / 16;
+    const uint32_t kb0 = 0, kb1 = blocks;
+    const uint32_t steps = (blocks + kChunk - 1) / kChunk;
 
     // ---- weights: pass i, lane l loads segment v = l + 64 i of the tile's
     // 16 row covers (row v / kVecs, segment v % kVecs); rows past the end
-    // are clamped onto the last one. A row's chunks all start `lead` bytes
-    // into their first segment; offsets are from tile + c0 * kBytes - 16 (so
-    // none is negative) and fit 32 bits (the launcher checks 16 rows do).
+    // are clamped onto the last one. Every chunk starts a whole multiple of
+    // 16 bytes into its row, so a row's chunks all start `lead` bytes into
+    // their first segment; offsets are from
+    // tile + c0 * kBytes - 16 (none negative) and fit 32 bits (the launcher
+    // checks 16 rows do).
     const uint8_t *tile = w + (uint64_t)t0 * row_bytes;
     auto lead_of = [&](uint32_t row) -> uint32_t {
         return (uint32_t)((reinterpret_cast<uintptr_t>(tile) + (uint64_t)row * row_bytes) & 15u);
@@ -328,36 +339,36 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
         off_full[i] = seg_off(v, kChunk);
         lds_dst[i] = min(v / kVecs, 15u) * kRowStride + (v % kVecs) * 16;
     }
-    u32x4 seg[kDepth][kPasses];
-    auto fetch_w = [&](u32x4 (&dst)[kPasses], uint32_t c0) {
-        const uint32_t nb = min(kChunk, blocks - c0);
+    u32x4 seg[kPasses];
+    auto fetch_w = [&](uint32_t c0) {
+        const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
         const uint8_t *base = tile + (uint64_t)c0 * kBytes - 16;
         if (nb == kChunk) {
 #pragma unroll
             for (int i = 0; i < (int)kPasses; ++i)
-                dst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off_full[i]));
+                seg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off_full[i]));
         } else {
 #pragma unroll
             for (int i = 0; i < (int)kPasses; ++i)
-                dst[i] = __builtin_nontemporal_load(
+                seg[i] = __builtin_nontemporal_load(
                     reinterpret_cast<const u32x4 *>(base + seg_off(lane + kWave * i, nb)));
         }
     };
 
-    // ---- x: wave wv stages rows wv, wv + 4, .. of the chunk (lane l: bytes
-    // 16 l .. 16 l + 15 of the row's 1 KB; past a partial chunk's end the
-    // last segment again)
+    // ---- x: the block's threads stage the chunk of the x rows (thread t,
+    // pass i: row (t + 256 i) / kXSegs, segment (t + 256 i) % kXSegs; past a
+    // partial chunk's end the last segment again)
     const uint16_t *x_tile = x + (uint64_t)r0 * in;
-    u32x4 xseg[kDepth][kXPasses];
-    auto fetch_x = [&](u32x4 (&dst)[kXPasses], uint32_t c0) {
-        const uint32_t nb = min(kChunk, blocks - c0);
-        const uint32_t sg = min(lane, nb * 4 - 1);
+    u32x4 xseg[kXPasses];
+    auto fetch_x = [&](uint32_t c0) {
+        const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
 #pragma unroll
         for (int i = 0; i < (int)kXPasses; ++i) {
-            const uint32_t xr = wv + kWaves * i;
+            const uint32_t flat = pt + kBlock * i, xr = flat / kXSegs;
+            const uint32_t sg = min(flat % kXSegs, nb * 4 - 1);
             if (xr < xrows)
-                dst[i] = *reinterpret_cast<const u32x4 *>(x_tile + (uint64_t)xr * in +
-                                                          (uint64_t)c0 * 32 + sg * 8);
+                xseg[i] = *reinterpret_cast<const u32x4 *>(x_tile + (uint64_t)xr * in +
+                                                           (uint64_t)c0 * 32 + sg * 8);
         }
     };
 
@@ -379,33 +390,28 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
 
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const half8 offset_b = __builtin_bit_cast(half8, u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u});
-    // chunks c+1 .. c+kDepth-1 are in flight while chunk c is computed;
-    // chunk c's registers are slot c % kDepth (the loop is unrolled by
-    // kDepth so the slot is static)
-#pragma unroll
-    for (int p = 0; p < kDepth; ++p)
-        if ((uint32_t)p * kChunk < blocks) {
-            fetch_w(seg[p], p * kChunk);
-            fetch_x(xseg[p], p * kChunk);
-        }
-    auto step = [&](auto pc, uint32_t c0) {
-        constexpr int p = decltype(pc)::value;
-        const uint32_t nb = min(kChunk, blocks - c0);
-        uint8_t *xbuf = xstage + ((c0 / kChunk) & 1u) * kXBuf;
+    if (kb0 < kb1) {
+        fetch_w(kb0);
+        fetch_x(kb0);
+    }
+    for (uint32_t step = 0; step < steps; ++step) {
+        const uint32_t c0 = kb0 + step * kChunk;
+        const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
+        uint8_t *xbuf = xstage[step & 1u];
 #pragma unroll
         for (int i = 0; i < (int)kPasses; ++i)
-            if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[p][i];
+            if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
 #pragma unroll
         for (int i = 0; i < (int)kXPasses; ++i) {
-            const uint32_t xr = wv + kWaves * i;
-            if (xr < xrows) *reinterpret_cast<u32x4 *>(xbuf + xr * kXRow + lane * 16) = xseg[p][i];
+            const uint32_t flat = pt + kBlock * i, xr = flat / kXSegs;
+            if (xr < xrows) *reinterpret_cast<u32x4 *>(xbuf + xr * kXRow + (flat % kXSegs) * 16) = xseg[i];
         }
         // every wave's x rows and this wave's weights are in LDS; every wave
-        // is past the chunk before the last, which read the other x buffer
+        // is past the step before the last, which read the other x buffer
         __syncthreads();
-        if (c0 + kDepth * kChunk < blocks) {
-            fetch_w(seg[p], c0 + kDepth * kChunk);
-            fetch_x(xseg[p], c0 + kDepth * kChunk);
+        if (c0 + kChunk < kb1) {
+            fetch_w(c0 + kChunk);
+            fetch_x(c0 + kChunk);
         }
         auto block = [&](auto jc) {
             constexpr int j = decltype(jc)::value;
@@ -452,12 +458,7 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
         // this wave's region is rewritten next: its reads come first
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
-    };
-    for (uint32_t c0 = 0; c0 < blocks; c0 += kDepth * kChunk)
-        static_for<kDepth>([&](auto pc) {
-            const uint32_t c = c0 + decltype(pc)::value * kChunk;
-            if (c < blocks) step(pc, c);
-        });
+    }
     if (o0 >= out) return;
     const uint32_t o = o0 + col;
     const float unit = kQ8 ? 16777216.0f : 1048576.0f;   // 2^24, 2^20
