@@ -15,6 +15,7 @@
 // (kind, dtype, shape, bias); calls run under one mutex because the bias
 // pointer is an attribute of the cached descriptor.
 #include "gemm.hpp"
+#include "kernels.hpp"
 
 #include "sdk.hpp"
 
@@ -133,9 +134,23 @@ bool make_plan(hipblasLtHandle_t handle, GemmKind kind, hipDataType type, uint64
 
 }  // namespace
 
+#ifndef ICSDK_GEMV_LINEAR
+#define ICSDK_GEMV_LINEAR 1
+#endif
+
 bool gemm(GemmKind kind, TensorDType dtype, const void *x, const void *w, const void *bias,
           void *y, size_t rows, size_t inner, size_t cols, hipStream_t stream, char *error,
           size_t capacity) {
+    if (ICSDK_GEMV_LINEAR && kind == GemmKind::kLinear && rows <= k::kGemvMaxRows) {
+        // decode-sized linears stream the weights through a GEMV kernel
+        const hipError_t e = k::linear_gemv(dtype == TENSOR_DTYPE_F32, x, w, bias, y, rows, inner,
+                                            cols, stream);
+        if (e == hipSuccess) return true;
+        if (e != hipErrorNotSupported) {
+            set_error(error, capacity, "GEMV launch failed: %s", hipGetErrorString(e));
+            return false;
+        }
+    }
     const hipDataType type = dtype == TENSOR_DTYPE_F32 ? HIP_R_32F : HIP_R_16F;
     GemmState &g = gemm_state();
     std::lock_guard<std::mutex> lock(g.mutex);

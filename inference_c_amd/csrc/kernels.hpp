@@ -73,6 +73,12 @@ size_t sum_max_partials_bytes(size_t n);
 // sum_max_f32_no_alloc() runs sum_max_f32 with it and refuses a launch whose
 // partials would not fit in scratch_bytes.
 size_t no_alloc_scratch_bytes();
+// Linear of at most kGemvMaxRows input rows as a GEMV over the weights
+// (k_linear.hip): hipErrorNotSupported when the shape or alignment does not
+// qualify (the caller then uses the GEMM library).
+constexpr size_t kGemvMaxRows = 4;
+hipError_t linear_gemv(bool f32, const void *x, const void *w, const void *bias, void *y,
+                       size_t rows, size_t in, size_t out, hipStream_t s);
 hipError_t no_alloc_scratch(void **ptr);
 hipError_t sum_max_f32_no_alloc(const float *x, size_t n, double *sum_out, float *max_out,
                                 void *scratch_ptr, size_t scratch_bytes, hipStream_t s);

@@ -65,6 +65,11 @@ LINEAR_SHAPES = [  # input shape, out features
     ((2, 5, 256), 96),      # rank-3 input
     ((512, 1024), 768),     # prefill
     ((17,), 40),            # rank-1 input
+    # the GEMV path (1-4 rows, in a whole number of 16-byte vectors): tail
+    # vectors only, odd output counts; whole unrolled steps; steps and a tail
+    ((4, 520), 130),
+    ((2, 2048), 33),
+    ((1, 8200), 9),
 ]
 
 
