@@ -6,7 +6,7 @@
 // 16 bytes holding weight j in the low nibble and weight j+16 in the high
 // nibble of byte j, stored as value + 8 (Q4_0, 18 bytes).
 //
-// quant_gemv_kernel (one input row) and quant_mma_kernel (two or more):
+// quant_gemv_kernel (one or two input rows) and quant_mma_kernel (three or more):
 // y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
 //
 // GEMV: a wave owns O output rows and walks them in chunks of 64 blocks.
@@ -74,47 +74,65 @@ struct GemvSel {
           s(sh ? 0x0c0c0302u : 0x0c0c0100u) {}
 };
 
-// sum_k x_k w_k of one block (f32) and its scale; x holds the block's 32 f16
-// as 16 pairs, xsum their sum.
-template <bool kQ8>
-__device__ inline float gemv_block(const uint8_t *chunk, uint32_t off, const GemvSel &sel,
-                                   const uint32_t (&x)[16], float xsum, float &scale) {
+// sum_k x_k w_k of one block (f32) for each of R input rows, and the
+// block's scale; x[r] holds row r's 32 f16 of the block as 16 pairs, xsum[r]
+// their sum. The weights are decoded once for the R rows.
+template <bool kQ8, int R>
+__device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const GemvSel &sel,
+                                  const uint32_t (&x)[R][16], const float (&xsum)[R], float &scale,
+                                  float (&dot)[R]) {
     constexpr int W = GemvFmt<kQ8>::kWin;
     const uint32_t *words = reinterpret_cast<const uint32_t *>(chunk + (off & ~3u));
     uint32_t e[W];
 #pragma unroll
     for (int i = 0; i < W; ++i) e[i] = words[i];
     scale = (float)__builtin_bit_cast(_Float16, (uint16_t)__builtin_amdgcn_perm(e[0], e[0], sel.s));
-    float s0 = 0.0f, s1 = 0.0f;
+    float s0[R], s1[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) s0[r] = s1[r] = 0.0f;
     if constexpr (kQ8) {
 #pragma unroll
         for (int i = 0; i < W; ++i) e[i] ^= 0x80808080u;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            s0 = __builtin_amdgcn_fdot2(as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.a)),
-                                        as_half2(x[2 * m]), s0, false);
-            s1 = __builtin_amdgcn_fdot2(as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.b)),
-                                        as_half2(x[2 * m + 1]), s1, false);
+            const half2_t pa = as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.a));
+            const half2_t pb = as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.b));
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                s0[r] = __builtin_amdgcn_fdot2(pa, as_half2(x[r][2 * m]), s0[r], false);
+                s1[r] = __builtin_amdgcn_fdot2(pb, as_half2(x[r][2 * m + 1]), s1[r], false);
+            }
         }
-        return __builtin_fmaf(s0 + s1, 16777216.0f, -128.0f * xsum);
+#pragma unroll
+        for (int r = 0; r < R; ++r) dot[r] = __builtin_fmaf(s0[r] + s1[r], 16777216.0f, -128.0f * xsum[r]);
     } else {
-        float h0 = 0.0f, h1 = 0.0f;
+        float h0[R], h1[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) h0[r] = h1[r] = 0.0f;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t pa = __builtin_amdgcn_perm(e[m + 1], e[m], sel.a);
             const uint32_t pb = __builtin_amdgcn_perm(e[m + 1], e[m], sel.b);
-            s0 = __builtin_amdgcn_fdot2(as_half2(pa & 0x000f000fu), as_half2(x[2 * m]), s0, false);
-            s1 = __builtin_amdgcn_fdot2(as_half2(pb & 0x000f000fu), as_half2(x[2 * m + 1]), s1, false);
-            h0 = __builtin_amdgcn_fdot2(as_half2(pa & 0x00f000f0u), as_half2(x[8 + 2 * m]), h0, false);
-            h1 = __builtin_amdgcn_fdot2(as_half2(pb & 0x00f000f0u), as_half2(x[8 + 2 * m + 1]), h1, false);
+            const half2_t la = as_half2(pa & 0x000f000fu), lb = as_half2(pb & 0x000f000fu);
+            const half2_t ha = as_half2(pa & 0x00f000f0u), hb = as_half2(pb & 0x00f000f0u);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                s0[r] = __builtin_amdgcn_fdot2(la, as_half2(x[r][2 * m]), s0[r], false);
+                s1[r] = __builtin_amdgcn_fdot2(lb, as_half2(x[r][2 * m + 1]), s1[r], false);
+                h0[r] = __builtin_amdgcn_fdot2(ha, as_half2(x[r][8 + 2 * m]), h0[r], false);
+                h1[r] = __builtin_amdgcn_fdot2(hb, as_half2(x[r][8 + 2 * m + 1]), h1[r], false);
+            }
         }
-        return __builtin_fmaf(__builtin_fmaf(h0 + h1, 0.0625f, s0 + s1), 16777216.0f, -8.0f * xsum);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            dot[r] = __builtin_fmaf(__builtin_fmaf(h0[r] + h1[r], 0.0625f, s0[r] + s1[r]), 16777216.0f,
+                                    -8.0f * xsum[r]);
     }
 }
 
-// Grid: x = waves of O output rows (4 waves per block), y = input rows.
-// Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
-template <bool kQ8, int O>
+// Grid: x = waves of O output rows (4 waves per block), y = groups of R
+// input rows. Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
+template <bool kQ8, int R, int O>
 __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
                                                             uint16_t *__restrict__ y,
@@ -130,10 +148,13 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         (blockIdx.x * kBlock + threadIdx.x) / kWave);
     const uint32_t o0 = wave * O;
     if (o0 >= out) return;
-    const uint32_t r = blockIdx.y;
+    const uint32_t r0 = blockIdx.y * R;
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
-    const uint16_t *xrow = x + (uint64_t)r * in;
+    // input rows past the end are clamped onto the last one (computed, not stored)
+    const uint16_t *xrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) xrow[r] = x + (uint64_t)min(r0 + r, rows - 1) * in;
     // rows past the end are clamped onto the last one (computed, not stored).
     // A chunk of 64 blocks is a whole number of 16-byte segments, so every
     // chunk of a row starts `lead` bytes into its first segment, and lane
@@ -153,9 +174,11 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
     // garbage, discarded.)
     const GemvSel sel_lead0((kBytes * lane) & 2u), sel_lead2((2 + kBytes * lane) & 2u);
 
-    float acc[O];
+    float acc[O][R];
 #pragma unroll
-    for (int o = 0; o < O; ++o) acc[o] = 0.0f;
+    for (int o = 0; o < O; ++o)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[o][r] = 0.0f;
 
     for (uint32_t c0 = 0; c0 < blocks; c0 += kWave) {
         const uint32_t nb = min((uint32_t)kWave, blocks - c0);
@@ -179,26 +202,28 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
             }
         }
         const uint32_t b = c0 + min(lane, nb - 1);
-        uint32_t xv[16];
-        {
-            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + (uint64_t)b * 32);
+        uint32_t xv[R][16];
+        float xsum[R];
+        const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow[r] + (uint64_t)b * 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const u32x4 t = xp[v];
-                xv[4 * v] = t.x;
-                xv[4 * v + 1] = t.y;
-                xv[4 * v + 2] = t.z;
-                xv[4 * v + 3] = t.w;
+                xv[r][4 * v] = t.x;
+                xv[r][4 * v + 1] = t.y;
+                xv[r][4 * v + 2] = t.z;
+                xv[r][4 * v + 3] = t.w;
             }
-        }
-        const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
-        float xs0 = 0.0f, xs1 = 0.0f;
+            float xs0 = 0.0f, xs1 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            xs0 = __builtin_amdgcn_fdot2(as_half2(xv[i]), one2, xs0, false);
-            xs1 = __builtin_amdgcn_fdot2(as_half2(xv[i + 1]), one2, xs1, false);
+            for (int i = 0; i < 16; i += 2) {
+                xs0 = __builtin_amdgcn_fdot2(as_half2(xv[r][i]), one2, xs0, false);
+                xs1 = __builtin_amdgcn_fdot2(as_half2(xv[r][i + 1]), one2, xs1, false);
+            }
+            xsum[r] = xs0 + xs1;
         }
-        const float xsum = xs0 + xs1;
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
@@ -214,22 +239,26 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 #pragma unroll
         for (int o = 0; o < O; ++o) {
             const uint32_t off = lead[o] + (b - c0) * kBytes;
-            float scale;
-            const float dot = gemv_block<kQ8>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0,
-                                              xv, xsum, scale);
+            float scale, dot[R];
+            gemv_block<kQ8, R>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0, xv, xsum, scale,
+                               dot);
             // a lane past the chunk's end adds 0 * (a finite dot): its scale
             // bytes may be anything, its decoded values are subnormals
-            acc[o] = __builtin_fmaf(live ? scale : 0.0f, dot, acc[o]);
+            const float sc = live ? scale : 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[o][r] = __builtin_fmaf(sc, dot[r], acc[o][r]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (int o = 0; o < O; ++o) {
-        const float total = wave_sum(acc[o]);
-        if (lane == 0 && o0 + o < out)
-            y[(uint64_t)r * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
-    }
+    for (int o = 0; o < O; ++o)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float total = wave_sum(acc[o][r]);
+            if (lane == 0 && o0 + o < out && r0 + r < rows)
+                y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+        }
 }
 
 // quant_mma_kernel (16 input rows per block row): each 32-weight block of 16
@@ -580,14 +609,15 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const uint16_t *__rest
     }
 }
 
-template <bool kQ8, int O>
+template <bool kQ8, int R, int O>
 hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
                        size_t in, size_t out, hipStream_t s) {
     constexpr uint32_t kWavesPerBlock = kBlock / kWave;
     const size_t waves = (out + O - 1) / O;
-    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock), (unsigned)rows);
-    quant_gemv_kernel<kQ8, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                      (uint32_t)out);
+    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock),
+                    (unsigned)((rows + R - 1) / R));
+    quant_gemv_kernel<kQ8, R, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                         (uint32_t)out);
     return hipGetLastError();
 }
 
@@ -616,16 +646,15 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
                                                                               (uint32_t)out);
         return hipGetLastError();
     }
-    // One input row: the GEMV, 4 output rows per wave (2, 6 and 8 measured
-    // slower for both formats); it has no x reuse to exploit, its dot
-    // products cost no more VALU per weight than the MFMA decode and it needs
-    // no x staging. Two or more: quant_mma_kernel decodes each weight once
-    // for up to 16 rows ([28672, 8192] Q8_0, 16 rows: 82 -> 58 us over a
-    // 16-row MFMA kernel that loaded x per wave; 4 rows 66 -> 49 us over a
-    // 4-row GEMV). Its 32-bit offsets bound `in`; past that every row takes
-    // the GEMV. Row groups per launch stay within the grid's y limit.
+    // One or two input rows: the GEMV, 4 output rows per wave (2, 6 and 8
+    // measured slower for both formats), decoding each weight once for the
+    // rows. From three rows quant_mma_kernel, which decodes each weight once
+    // for up to 16 ([28672, 8192] Q8_0: 2 rows 51 us GEMV vs 56 MFMA; 4 rows
+    // 64 vs 52; Q4_0 2 rows 39 vs 44, 4 rows 52 vs 40). Its 32-bit offsets
+    // bound `in`; past that every row takes the 1-row GEMV. Row groups per
+    // launch stay within the grid's y limit.
     constexpr size_t kMaxGroups = 65535;
-    const bool mma = rows >= 2 && in <= (size_t{1} << 25);
+    const bool mma = rows > 2 && in <= (size_t{1} << 25);
     for (size_t r0 = 0; r0 < rows;) {
         const size_t left = rows - r0;
         hipError_t status;
@@ -633,9 +662,12 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
         if (mma) {
             done = left < kMaxGroups * 16 ? left : kMaxGroups * 16;
             status = launch_mma<kQ8>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+        } else if (left == 2) {
+            done = 2;
+            status = launch_gemv<kQ8, 2, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else {
             done = left < kMaxGroups ? left : kMaxGroups;
-            status = launch_gemv<kQ8, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+            status = launch_gemv<kQ8, 1, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;
