@@ -200,12 +200,14 @@ __global__ __launch_bounds__(kBlock) void sdpa_row_kernel(const S *__restrict__ 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-// A block owns BM queries of one (batch, head): 32 per wave. Keys come in
-// tiles of 64, staged in LDS by the whole block, double-buffered: the next
-// tile's global loads are issued before the current tile is computed and
-// land in the other buffer afterwards, so one barrier per tile separates the
-// writers of a buffer from its readers. K is stored as [key][dim] rows, V
-// transposed as [dim][slot] with the slot order below.
+// A block owns BM queries of one (batch, head): 32 per wave (KS waves per
+// 32 queries when the key tiles are split between them). Keys come in tiles
+// of 64, staged in LDS by the whole block, double-buffered: the next step's
+// global loads are issued before the current step is computed and land in
+// the other buffer afterwards, so one barrier per step separates the
+// writers of a buffer from its readers. K and V are both stored as
+// [key][dim] rows, as they are in memory (16-byte loads and stores, 256
+// contiguous bytes per row at D 128).
 //
 // v_mfma_f32_32x32x16_f16 lane layout (checked on the device): A[m][k] in
 // lane l at m = l % 32, k = 8 (l / 32) + i; B[k][n] at n = l % 32,
@@ -216,9 +218,14 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 // half tile, keys 8 (r / 4) + 4 (l / 32) + r % 4; lane l ^ 32 holds the rest.
 // The online softmax runs per lane pair (one swizzle for the max, one for
 // the sum). P^T is then already the B operand of out^T = V^T P^T: chunk c of
-// its k dimension is p[8c .. 8c + 7], keys 16c + 8 (i / 4) + 4 (l / 32) + i % 4,
-// and V^T is stored with that key order (slot 16c + 8h + i), so each A
-// fragment is one 16-byte LDS read.
+// its k dimension is p[8c .. 8c + 7], keys 16c + 8 (i / 4) + 4 (l / 32) + i % 4.
+// The matching A fragment (V^T: lane l needs V[16c + 4h + k][d] and
+// V[16c + 8 + 4h + k][d], k = 0..3, d = l % 32, h = l / 32) comes from the
+// [key][dim] V rows through two ds_read_b64_tr_b16: within each 16-lane
+// group that instruction hands lane j element j % 4 of the 4-element vectors
+// addressed by lanes j / 4 + 4k, k = 0..3 (checked on the device), so lane
+// i of group g addresses row 16c + 4 (g / 2) + i / 4 (+ 8), columns
+// 16 (g % 2) + 4 (i % 4) .. + 3.
 constexpr int kFlashN = 64;    // keys per tile
 constexpr float kLazyLog2 = 8.0f;   // rescale when a row maximum grows by more than 2^8
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt at their no-wait maxima)
@@ -289,15 +296,16 @@ __device__ inline float pair_sum(float v) {
 // Each MFMA then consumes a fragment read kAhead MFMAs earlier (~128
 // cycles), which covers the LDS latency; left to itself the scheduler reads
 // one fragment ahead and every MFMA waits for its read.
-template <int N>
+// (R LDS reads per MFMA.)
+template <int N, int R = 1>
 __device__ inline void lds_read_ahead() {
     constexpr int kAhead = 4;
     constexpr int kMfma = 0x008, kDsRead = 0x100;
-    __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead * R, 0);
 #pragma unroll
     for (int i = 0; i < N - kAhead; ++i) {
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, R, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
 }
@@ -316,9 +324,13 @@ __device__ inline void mfma_phase_end() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-__device__ inline uint32_t vt_slot(uint32_t key) {
-    const uint32_t within = key % 16;
-    return (key / 16) * 16 + 8 * ((within / 4) % 2) + (within / 8) * 4 + within % 4;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Four halves through the LDS transpose read (lane layout above).
+__device__ inline half4 lds_read_tr(const _Float16 *p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v *)(p));
+    return __builtin_bit_cast(half4, r);
 }
 
 // A split block's result for one query: its lane pair holds the query's
@@ -416,33 +428,44 @@ __global__ __launch_bounds__(kBlock) void sdpa_combine_kernel(SdpaArgs a, S *__r
     }
 }
 
-template <int D, int BM, bool kMask, bool kSplit>
-__global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__restrict__ q,
+template <int D, int BM, bool kMask, bool kSplit, int KS>
+__global__ __launch_bounds__(BM * 2 * KS) void sdpa_flash_kernel(const _Float16 *__restrict__ q,
                                                             const _Float16 *__restrict__ k,
                                                             const _Float16 *__restrict__ v,
                                                             const _Float16 *__restrict__ mask,
                                                             _Float16 *__restrict__ out,
                                                             SdpaArgs a) {
-    constexpr int THREADS = BM * 2;          // one wave per 32 queries
-    constexpr uint32_t kTileKeys = kFlashN;
+    constexpr int QW = BM / 32;              // query groups of 32: one wave each per key part
+    constexpr int THREADS = BM * 2 * KS;
     constexpr int KC = D / 16;               // 16-dim chunks of Q K^T
     constexpr int VT = D / 32;               // 32-row tiles of out^T
     constexpr int KROW = D + 8;              // LDS row of K (halves)
-    constexpr int VROW = kFlashN + 8;        // LDS row of V^T (halves)
-    constexpr int VECS = kFlashN * D / 8;    // 16-byte vectors per K or V tile
-    constexpr int PER = VECS / THREADS;      // per thread, per tile, per operand
+    // LDS row of V (halves): 16 (D 128) or 48 (D 64) dwords past a multiple
+    // of 64, so the 4 rows a transpose read takes per half wave start 16
+    // banks apart (conflict-free)
+    constexpr int VROW = D + 32;
+    constexpr int KTILE = kFlashN * KROW;    // LDS halves of one K tile
+    constexpr int VTILE = kFlashN * VROW;    // LDS halves of one V tile
+    constexpr int TV = kFlashN * D / 8;      // 16-byte vectors per K or V tile
+    constexpr int VECS = KS * TV;            // per operand and step (KS tiles)
+    constexpr int PER = VECS / THREADS;      // per thread, per step, per operand
     static_assert(VECS % THREADS == 0, "tile load split");
-    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashN * KROW];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[2][D * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][KS * KTILE];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[2][KS * VTILE];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
+    // wave w takes query group w % QW and key tile kpart of every step
+    const uint32_t qgroup = wave % QW, kpart = wave / QW;
     const uint32_t col = lane & 31, half = lane >> 5;
+    // the lane's transpose-read address in a V tile (chunk 0, d tile 0)
+    const uint32_t v_lane =
+        (4 * (lane / 32) + (lane % 16) / 4) * VROW + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
     const FlashItem item = flash_item(a, blockIdx.x);
     const uint32_t qblock = item.qblock, bh = item.bh;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
-    const uint32_t qw = qblock * BM + wave * 32;        // the wave's first query
+    const uint32_t qw = qblock * BM + qgroup * 32;      // the wave's first query
     const uint32_t qi = qw + col;                       // the lane's query
     const bool q_live = qi < a.ql;
     const float neg_inf = -__builtin_inff();
@@ -479,54 +502,58 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
     const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
 
-    // tile loads: thread `tid` moves vectors tid, tid + THREADS, ... of K
-    // (row-major: key, 8-dim group) and of V (key-fastest, for the transpose)
+    // tile loads of a step (KS tiles from key k0): thread `tid` moves vectors
+    // tid, tid + THREADS, ... of K and of V (per tile row-major: key, 8-dim
+    // group). The loads take no branch:
+    // rows past the end are clamped onto the last key and zeroed when
+    // stashed. (A fetch with a bounds-tested branch per load let the
+    // compiler merge the whole-tile loads into that path, behind a wait for
+    // every load just issued: the prefetch no longer overlapped the tile's
+    // MFMAs, 15-20% slower.)
     half8 kreg[PER], vreg[PER];
     auto fetch = [&](uint32_t k0) {
-        if (k0 + kFlashN <= a.kl) {   // a whole tile: no per-row bounds test
-#pragma unroll
-            for (int u = 0; u < PER; ++u) {
-                const uint32_t e = tid + u * THREADS;
-                const uint32_t kk = k0 + e / (D / 8), kc = e % (D / 8);
-                const uint32_t vk = k0 + e % kFlashN, vc = e / kFlashN;
-                kreg[u] = *reinterpret_cast<const half8 *>(k + (kv_base + kk) * D + kc * 8);
-                vreg[u] = *reinterpret_cast<const half8 *>(v + (kv_base + vk) * D + vc * 8);
-            }
-            return;
-        }
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const uint32_t e = tid + u * THREADS;
-            const uint32_t kk = k0 + e / (D / 8), kc = e % (D / 8);
-            const uint32_t vk = k0 + e % kFlashN, vc = e / kFlashN;
-            kreg[u] = kk < a.kl ? *reinterpret_cast<const half8 *>(k + (kv_base + kk) * D + kc * 8)
-                                : half8{};
-            vreg[u] = vk < a.kl ? *reinterpret_cast<const half8 *>(v + (kv_base + vk) * D + vc * 8)
-                                : half8{};
+            const uint32_t e = tid + u * THREADS, tk = k0 + e / TV * kFlashN, r = e % TV;
+            const size_t row = (kv_base + min(tk + r / (D / 8), a.kl - 1)) * D + r % (D / 8) * 8;
+            kreg[u] = *reinterpret_cast<const half8 *>(k + row);
+            vreg[u] = *reinterpret_cast<const half8 *>(v + row);
         }
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](int buf, uint32_t k0) {
+        if (k0 + KS * kFlashN > a.kl) {   // a ragged last step: zero the rows past the end
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const uint32_t e = tid + u * THREADS, tk = k0 + e / TV * kFlashN, r = e % TV;
+                if (tk + r / (D / 8) >= a.kl) {
+                    kreg[u] = half8{};
+                    vreg[u] = half8{};
+                }
+            }
+        }
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const uint32_t e = tid + u * THREADS;
-            *reinterpret_cast<half8 *>(&ks[buf][(e / (D / 8)) * KROW + (e % (D / 8)) * 8]) = kreg[u];
-            const uint32_t slot = vt_slot(e % kFlashN), vc = e / kFlashN;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vs[buf][(vc * 8 + i) * VROW + slot] = vreg[u][i];
+            const uint32_t e = tid + u * THREADS, tile = e / TV, r = e % TV;
+            *reinterpret_cast<half8 *>(&ks[buf][tile * KTILE + (r / (D / 8)) * KROW + (r % (D / 8)) * 8]) =
+                kreg[u];
+            *reinterpret_cast<half8 *>(&vs[buf][tile * VTILE + (r / (D / 8)) * VROW + (r % (D / 8)) * 8]) =
+                vreg[u];
         }
     };
 
     if (t_begin < tiles) {
-        fetch(t_begin * kTileKeys);
-        stash(t_begin & 1);
+        fetch(t_begin * kFlashN);
+        stash(0, t_begin * kFlashN);
     }
     __syncthreads();
-    for (uint32_t t = t_begin; t < tiles; ++t) {
-        const int buf = t & 1;
+    // step: KS tiles from t0; this wave takes tile t0 + kpart
+    for (uint32_t t0 = t_begin, step = 0; t0 < tiles; t0 += KS, ++step) {
+        const int buf = step & 1;
+        const uint32_t t = t0 + kpart;
         const uint32_t k0 = t * kFlashN;
-        const bool more = t + 1 < tiles;
-        if (more) fetch(k0 + kFlashN);
-        if (wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
+        const bool more = t0 + KS < tiles;
+        if (more) fetch((t0 + KS) * kFlashN);
+        if (t < tiles && wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
             // interior tile: every key exists and is visible to every query of
             // the wave, so no per-score bounds or causal test is needed
             const bool interior = k0 + kFlashN <= a.kl &&
@@ -544,7 +571,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
 #pragma unroll
                 for (int hblk = 0; hblk < 2; ++hblk) {
                     const half8 kf = *reinterpret_cast<const half8 *>(
-                        &ks[buf][(32 * hblk + col) * KROW + 16 * c + 8 * half]);
+                        &ks[buf][kpart * KTILE + (32 * hblk + col) * KROW + 16 * c + 8 * half]);
                     st[hblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], st[hblk], 0, 0, 0);
                 }
             lds_read_ahead<2 * KC>();
@@ -651,17 +678,56 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_kernel(const _Float16 *__re
             for (int c = 0; c < 4; ++c)
 #pragma unroll
                 for (int tt = 0; tt < VT; ++tt) {
-                    const half8 vf = *reinterpret_cast<const half8 *>(
-                        &vs[buf][(32 * tt + col) * VROW + 16 * c + 8 * half]);
+                    const _Float16 *vp = &vs[buf][kpart * VTILE + 16 * c * VROW + v_lane + 32 * tt];
+                    const half4 lo = lds_read_tr(vp), hi = lds_read_tr(vp + 8 * VROW);
+                    const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[tt], 0, 0, 0);
                 }
-            lds_read_ahead<4 * VT>();
+            lds_read_ahead<4 * VT, 2>();
             mfma_phase_end();
         }
-        if (more) stash(buf ^ 1);
+        if (more) stash(buf ^ 1, (t0 + KS) * kFlashN);
         __syncthreads();
     }
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
+    if constexpr (KS == 2) {
+        // Merge the two key parts of each query group through LDS (the loop
+        // ended on a barrier, so the tile buffers are free): the part-1 wave
+        // leaves its (o, m, l, NaN flag), the part-0 wave folds them in with
+        // the merge rules of sdpa_combine_kernel and goes on alone.
+        static_assert(QW * (VT * 4 + 1) * kWave * 16 <= sizeof(ks), "merge area");
+        f32x4 *xch = reinterpret_cast<f32x4 *>(&ks[0][0]) + qgroup * (VT * 4 + 1) * kWave + lane;
+        if (kpart == 1) {
+#pragma unroll
+            for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    xch[(tt * 4 + g) * kWave] =
+                        f32x4{o[tt][4 * g], o[tt][4 * g + 1], o[tt][4 * g + 2], o[tt][4 * g + 3]};
+            xch[VT * 4 * kWave] = f32x4{m, l, nan_seen ? 1.0f : 0.0f, 0.0f};
+        }
+        __syncthreads();
+        if (kpart == 1) return;
+        const f32x4 other = xch[VT * 4 * kWave];
+        const float big = fmaxf(m, other.x);
+        // weights 2^(m_s - M); a part that saw nothing (m_s = -inf), and
+        // every part of a row whose M is not finite (a zero row), weigh 0
+        const bool finite = __builtin_isfinite(big);
+        const float w0 = !finite || m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - big);
+        const float w1 = !finite || other.x == -__builtin_inff() ? 0.0f
+                                                                  : __builtin_amdgcn_exp2f(other.x - big);
+#pragma unroll
+        for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 p = xch[(tt * 4 + g) * kWave];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[tt][4 * g + j] = w0 * o[tt][4 * g + j] + w1 * p[j];
+            }
+        l = w0 * l + w1 * other.y;
+        m = big;
+        nan_seen = nan_seen || other.z != 0.0f;
+    }
     if (!q_live) return;
     if constexpr (kSplit) {
         if (item.parts > 1) {
@@ -964,6 +1030,7 @@ namespace {
 struct FlashPlan {
     bool flash = false;
     uint32_t bm = 64, tk = 64;   // queries per block (64, 128, or 256 for f16), keys per tile
+    uint32_t key_parts = 1;      // f16: waves per query group, taking alternate key tiles
     uint32_t qblocks = 0, items = 0;
     uint32_t split_tiles = 0;
     uint32_t max_parts = 1;
@@ -971,6 +1038,33 @@ struct FlashPlan {
     bool table = false, xcd_heads = false;
     uint32_t item[kMaxFlashItems] = {};
 };
+
+// f16 blocks of 128 queries whose 8 waves split the key tiles in two (see
+// sdpa_flash_kernel) pay where a causal launch is about one round of
+// 256-query blocks with uneven key ranges: twice as many blocks, each half
+// as long, let the longest-first order pair long blocks with short ones on
+// a CU, with no merge launch. Measured (us, two-part vs 256-query blocks):
+// 32q/8kv 2048^2 D 128 causal 58.4 vs 70.3, D 64 37.3 vs 50.0; 32 x 1024^2
+// D 64 causal 17.5 vs 22.4 (128-query blocks). Each two-part step stages
+// twice the K/V bytes per wave, so where the key ranges are even, or there
+// are several rounds of blocks for the order to balance, they lose: 2048^2
+// D 128 non-causal 95 vs 80, 4096^2 causal 187 vs 167, 4 x 2048^2 causal
+// 220 vs 189.
+bool key_parts_pay(const k::SdpaShape &sh, bool causal) {
+    const size_t bhs = sh.batch * sh.q_heads;
+    if (!causal || ((sh.q_len + 127) / 128) * bhs < 256 || ((sh.q_len + 255) / 256) * bhs > 256)
+        return false;
+    // uneven: the longest 256-query block sees > 5/4 of the average key tiles
+    const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
+    const uint32_t offset = kl > ql ? kl - ql : 0, blocks = (ql + 255) / 256;
+    uint64_t total = 0, most = 0;
+    for (uint32_t j = 0; j < blocks; ++j) {
+        const uint64_t t = flash_tiles(ql, kl, true, offset, 256, kFlashN, j);
+        total += t;
+        most = t > most ? t : most;
+    }
+    return 4 * most * blocks > 5 * total;
+}
 
 FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal, bool split) {
     FlashPlan p;
@@ -982,7 +1076,10 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
-    if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
+    if (!f32 && key_parts_pay(sh, causal)) {
+        p.bm = 128;
+        p.key_parts = 2;
+    } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
     else if (((sh.q_len + 127) / 128) * bhs >= 64) p.bm = 128;
     else p.bm = 64;
     p.tk = f32 ? 32 : 64;
@@ -994,7 +1091,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0;
     auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
-    if (split) {
+    if (split && p.key_parts == 1) {
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
@@ -1097,7 +1194,7 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
 }  // namespace
 
 // One flash launch for the plan's (D, BM) with the general (mask) / split
-// variant.
+// variant; the f16 kernel also takes its key parts per query group (KS).
 #define ICSDK_FLASH_VARIANTS(KERNEL, D, BM, Q, K, V, M, O)                                         \
     do {                                                                                           \
         if (general && split)                                                                      \
@@ -1109,6 +1206,22 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             hipLaunchKernelGGL((KERNEL<D, BM, false, false>), grid, block, 0, s, Q, K, V, M, O, a);\
     } while (0)
+#define ICSDK_FLASH_VARIANTS_KS(KERNEL, D, BM, KS, Q, K, V, M, O)                                  \
+    do {                                                                                           \
+        if (general && split)                                                                      \
+            hipLaunchKernelGGL((KERNEL<D, BM, true, true, KS>), grid, block, 0, s, Q, K, V, M, O, a);  \
+        else if (general)                                                                          \
+            hipLaunchKernelGGL((KERNEL<D, BM, true, false, KS>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else if (split)                                                                            \
+            hipLaunchKernelGGL((KERNEL<D, BM, false, true, KS>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else                                                                                       \
+            hipLaunchKernelGGL((KERNEL<D, BM, false, false, KS>), grid, block, 0, s, Q, K, V, M, O, a);\
+    } while (0)
+// two key parts: the raw-product, unsplit variant only (a plan with two key
+// parts splits no query block; the general variant would not fit two waves
+// per SIMD at D 128 and runs with one key part)
+#define ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O)                                         \
+    hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a)
 #define ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O)                                                  \
     do {                                                                                           \
         if (shape.head_dim == 64) {                                                                \
@@ -1119,14 +1232,21 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
             else ICSDK_FLASH_VARIANTS(KERNEL, 128, 64, Q, K, V, M, O);                             \
         }                                                                                          \
     } while (0)
-// the same with 256-query blocks (f16 only)
-#define ICSDK_FLASH_SHAPES_256(KERNEL, Q, K, V, M, O)                                              \
+// the f16 kernel: 64-, 128- or 256-query blocks, 128-query blocks with two
+// key parts per query group
+#define ICSDK_FLASH_SHAPES_F16(KERNEL, Q, K, V, M, O)                                              \
     do {                                                                                           \
-        if (plan.bm == 256) {                                                                      \
-            if (shape.head_dim == 64) ICSDK_FLASH_VARIANTS(KERNEL, 64, 256, Q, K, V, M, O);        \
-            else ICSDK_FLASH_VARIANTS(KERNEL, 128, 256, Q, K, V, M, O);                            \
+        const int bm = (int)plan.bm;                                                               \
+        if (shape.head_dim == 64) {                                                                \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 64, Q, K, V, M, O);                      \
+            else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 256, 1, Q, K, V, M, O);        \
+            else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 128, 1, Q, K, V, M, O);        \
+            else ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 64, 1, Q, K, V, M, O);                        \
         } else {                                                                                   \
-            ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O);                                             \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 128, Q, K, V, M, O);                     \
+            else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 256, 1, Q, K, V, M, O);       \
+            else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 128, 1, Q, K, V, M, O);       \
+            else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
         }                                                                                          \
     } while (0)
 
@@ -1166,16 +1286,19 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     // the raw-product softmax needs scale > 0; other scales take the general
     // (mask) variant, whose mask may be null
     const bool general = mask != nullptr || !(scale > 0.0f);
-    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm);
-    ICSDK_FLASH_SHAPES_256(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
+    const uint32_t ks = general ? 1 : plan.key_parts;
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm * ks);
+    ICSDK_FLASH_SHAPES_F16(sdpa_flash_kernel, h(q), h(k), h(v), h(mask), o16);
     const hipError_t status = hipGetLastError();
     return status != hipSuccess || !split ? status : combine_splits(a, plan, o16, s);
 }
 
 }  // namespace k
 
-#undef ICSDK_FLASH_SHAPES_256
+#undef ICSDK_FLASH_SHAPES_F16
 #undef ICSDK_FLASH_SHAPES
+#undef ICSDK_FLASH_VARIANTS_KS2
+#undef ICSDK_FLASH_VARIANTS_KS
 #undef ICSDK_FLASH_VARIANTS
 
 

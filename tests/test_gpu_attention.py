@@ -264,3 +264,77 @@ def test_split_key_range_special_rows(sdk, orc, dtype):
     np.testing.assert_array_equal(got[0, 0, 0], v[0, 0, 900].astype(got.dtype))
     weight = orc.sdpa_abs_weight(q, k, v, mask, 0.125, False)
     check(got[0, 0, 3:], want[0, 0, 3:], weight[0, 0, 3:], dtype, "ordinary row")
+
+
+# f16 causal shapes whose 256-query blocks would be about one round on the
+# GPU with uneven key ranges: blocks of 128 queries whose 8 waves take 4
+# query groups x 2 key parts (alternate 64-key tiles), merged in LDS.
+# The oracle runs on the first and the last kv head's query heads only.
+KEY_PART_SHAPES = [
+    (1, 128, 16, 512, 512, 64, 64),     # 4 and 8 key tiles per 256 queries
+    (2, 64, 16, 512, 512, 128, 128),    # batch 2, D 128
+    (1, 128, 32, 500, 500, 64, 64),     # ragged query and key tiles
+    (1, 64, 16, 700, 720, 64, 64),      # kv longer than q (causal offset 20), ragged
+    (1, 64, 64, 512, 512, 128, 128),    # one q head per kv head
+]
+
+
+def head_subset(q, k, v, got):
+    """(q, k, v, got) restricted to the query heads of kv heads 0 and -1."""
+    group = q.shape[1] // k.shape[1]
+    qs = np.r_[0:group, q.shape[1] - group:q.shape[1]]
+    ks = np.r_[0:1, k.shape[1] - 1:k.shape[1]]
+    return q[:, qs], k[:, ks], v[:, ks], got[:, qs]
+
+
+@pytest.mark.parametrize("shape", KEY_PART_SHAPES)
+def test_key_parts(sdk, orc, shape):
+    q, k, v, _ = inputs(orc, shape, "f16", 34, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, None, scale, True, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, scale, True)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, True)
+    check(got, want, weight, "f16", f"{shape} causal")
+
+
+@pytest.mark.parametrize("direction", [1.0, -1.0])
+def test_key_parts_growing_row_maxima(sdk, orc, direction):
+    """Scores climbing (or falling) 60 log2 units along the keys: the two
+    key parts' running maxima move at different tiles and are merged with
+    their own weights."""
+    shape = (1, 128, 16, 512, 512, 64, 64)
+    q, k, v, _ = inputs(orc, shape, "f16", 35, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    reach = 60.0 / (4.0 * scale * np.log2(np.e))
+    q[..., 0] = 4.0
+    k[..., :, 0] = (direction * reach * np.arange(shape[4]) / shape[4]).astype(k.dtype)
+    got = run_device(sdk, q, k, v, None, scale, True, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, scale, True)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, True)
+    check(got, want, weight, "f16", f"direction={direction}")
+
+
+def test_key_parts_special_rows(sdk, orc):
+    """Special rows across the two key parts, bitwise vs the oracle: a NaN
+    query (every score NaN: zero row); a NaN key in the second part's first
+    tile (rows that see it are NaN); a +inf key component in the second
+    part's second tile (rows that see it with a positive query component:
+    max +inf, zero row; negative: -inf score, the key drops out)."""
+    shape = (1, 128, 16, 512, 512, 64, 64)
+    q, k, v, _ = inputs(orc, shape, "f16", 36, False)
+    q[0, 0, 1, 5] = np.nan
+    k[0, 15, 70, 3] = np.nan
+    k[0, 15, 200, 0] = np.inf
+    got = run_device(sdk, q, k, v, None, 0.125, True, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, 0.125, True)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    zero = (want == 0).all(axis=-1)
+    assert zero[0, 0, 1] and zero[0, -1].any()
+    assert (got[zero] == 0).all()
+    weight = orc.sdpa_abs_weight(q, k, v, None, 0.125, True)
+    live = ~zero & ~np.isnan(want).any(axis=-1)
+    assert live[0, -1, :70].all()
+    check(got[live], want[live], weight[live], "f16", "ordinary rows")
