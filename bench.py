@@ -517,8 +517,8 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
                     lambda s, fmt=fmt: sdk.call(f"tensor_linear_{fmt}_f16", s[1], s[0], s[2]),
                     host_w.nbytes + rows * (in_f + out_f) * 2, rows * out_f)
         del host_w
-    # f16 linear through hipBLASLt: a decode row (HBM-bound GEMV on the
-    # weights) and a 4096-token prefill (MFMA-bound)
+    # f16 linear: a decode row (the GEMV kernel, HBM-bound on the weights)
+    # and a 4096-token prefill (hipBLASLt, MFMA-bound)
     def linear_set(rows, inw, out_f):
         return lambda: (filled("f16", (rows, inw), "normal", 8, 0, 0.0, 1.0),
                         filled("f16", (out_f, inw), "normal", 8, 1, 0.0, 0.02),
@@ -697,6 +697,22 @@ def pmc_probe(sdk, reps=3):
     del packed
     ops.append(("linear_q8_0_f16_1x8192_to_28672",
                 lambda: sdk.call("tensor_linear_q8_0_f16", t["x8"], t["w8"], t["y8"])))
+    # the same weights times 4 rows (the MFMA kernel), the Q4_0 decode GEMV
+    # and the f16 decode linear (GEMV kernel)
+    t["x84"], t["y84"] = filled("f16", (4, 8192), "normal", 7, 4, 0.0, 1.0), T("f16", (4, 28672))
+    ops.append(("linear_q8_0_f16_4x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q8_0_f16", t["x84"], t["w8"], t["y84"])))
+    packed = np.random.default_rng(8).integers(0, 256, size=(28672, 256, 18), dtype=np.uint8)
+    packed[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
+    t["w4"] = T("u8", packed.shape).upload(packed)
+    t["y4"] = T("f16", (1, 28672))
+    del packed
+    ops.append(("linear_q4_0_f16_1x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q4_0_f16", t["x8"], t["w4"], t["y4"])))
+    t["wl"] = filled("f16", (8192, 8192), "normal", 7, 5, 0.0, 0.01)
+    t["yl"] = T("f16", (1, 8192))
+    ops.append(("linear_f16_1x8192_to_8192",
+                lambda: sdk.call("tensor_linear_f16", t["x8"], t["wl"], None, t["yl"])))
     # a [4096, 4096] f16 transpose (64x64 LDS tiles)
     t["xt"], t["yt"] = filled("f16", (4096, 4096), "normal", 4, 0, 0.0, 1.0), T("f16", (4096, 4096))
     transpose = TensorView.make((4096, 4096), (1, 4096), 0)
