@@ -767,33 +767,37 @@ __global__ __launch_bounds__(BM * 2 * KS) void sdpa_flash_kernel(const _Float16 
 // the sum, with the special-row rules of the f16 kernel.
 constexpr int kFlashN32 = 32;   // keys per f32 tile
 
-template <int D, int BM, bool kMask, bool kSplit>
-__global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__restrict__ q,
+template <int D, int BM, bool kMask, bool kSplit, int KS>
+__global__ __launch_bounds__(BM * 2 * KS) void sdpa_flash_f32_kernel(const float *__restrict__ q,
                                                                 const float *__restrict__ k,
                                                                 const float *__restrict__ v,
                                                                 const float *__restrict__ mask,
                                                                 float *__restrict__ out,
                                                                 SdpaArgs a) {
-    constexpr int THREADS = BM * 2;
+    constexpr int QW = BM / 32;              // query groups of 32: one wave each per key part
+    constexpr int THREADS = BM * 2 * KS;
     constexpr int KN = kFlashN32;
-    constexpr uint32_t kTileKeys = KN;
     constexpr int ROW = D + 4;               // LDS row (floats)
     constexpr int VT = D / 32;               // 32-row tiles of out^T
     constexpr int QC = D / 2;                // MFMAs of S^T per tile
-    constexpr int VECS = KN * D / 4;         // float4 vectors per K or V tile
+    constexpr int TILE = KN * ROW;           // LDS floats of one K or V tile
+    constexpr int TV = KN * D / 4;           // float4 vectors per K or V tile
+    constexpr int VECS = KS * TV;            // per operand and step (KS tiles)
     constexpr int PER = VECS / THREADS;
     static_assert(VECS % THREADS == 0, "tile load split");
-    __shared__ __attribute__((aligned(16))) float ks[2][KN * ROW];
-    __shared__ __attribute__((aligned(16))) float vs[2][KN * ROW];
+    // step buffer b: K tiles at lds[b * 2 KS TILE], V tiles KS TILE further
+    __shared__ __attribute__((aligned(16))) float lds[2 * 2 * KS * TILE];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
+    // wave w takes query group w % QW and key tile kpart of every step
+    const uint32_t qgroup = wave % QW, kpart = wave / QW;
     const uint32_t col = lane & 31, half = lane >> 5;
     const FlashItem item = flash_item(a, blockIdx.x);
     const uint32_t qblock = item.qblock, bh = item.bh;
     const uint32_t head = bh % a.qh, b = bh / a.qh;
     const size_t kv_base = ((size_t)b * a.kvh + head / a.group) * a.kl;
-    const uint32_t qw = qblock * BM + wave * 32;
+    const uint32_t qw = qblock * BM + qgroup * 32;
     const uint32_t qi = qw + col;
     const bool q_live = qi < a.ql;
     const float neg_inf = -__builtin_inff();
@@ -831,39 +835,54 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
     const uint64_t wave_last_key = (uint64_t)min(qw + 31, a.ql - 1) + a.causal_offset;
     const uint64_t lane_last_key = (uint64_t)qi + a.causal_offset;
 
-    // tile loads: vector e of a tile is key e / (D/4), floats 4 (e % (D/4)) ...
+    // tile loads of a step (KS tiles from key k0): vector e of a tile is key
+    // e / (D/4), floats 4 (e % (D/4)) ...; branch-free (rows past the end
+    // clamped onto the last key, zeroed when stored: see the f16 kernel)
     f32x4 kreg[PER], vreg[PER];
     auto fetch = [&](uint32_t k0) {
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const uint32_t e = tid + u * THREADS;
-            const uint32_t kk = k0 + e / (D / 4), part = e % (D / 4);
-            const size_t at = (kv_base + kk) * D + part * 4;
-            kreg[u] = kk < a.kl ? *reinterpret_cast<const f32x4 *>(k + at) : f32x4{0, 0, 0, 0};
-            vreg[u] = kk < a.kl ? *reinterpret_cast<const f32x4 *>(v + at) : f32x4{0, 0, 0, 0};
+            const uint32_t e = tid + u * THREADS, tk = k0 + e / TV * KN, r = e % TV;
+            const size_t at = (kv_base + min(tk + r / (D / 4), a.kl - 1)) * D + (r % (D / 4)) * 4;
+            kreg[u] = *reinterpret_cast<const f32x4 *>(k + at);
+            vreg[u] = *reinterpret_cast<const f32x4 *>(v + at);
         }
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](int buf, uint32_t k0) {
+        if (k0 + KS * KN > a.kl) {   // a ragged last step: zero the rows past the end
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const uint32_t e = tid + u * THREADS, tk = k0 + e / TV * KN, r = e % TV;
+                if (tk + r / (D / 4) >= a.kl) {
+                    kreg[u] = f32x4{0, 0, 0, 0};
+                    vreg[u] = f32x4{0, 0, 0, 0};
+                }
+            }
+        }
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const uint32_t e = tid + u * THREADS;
-            const uint32_t at = (e / (D / 4)) * ROW + (e % (D / 4)) * 4;
-            *reinterpret_cast<f32x4 *>(&ks[buf][at]) = kreg[u];
-            *reinterpret_cast<f32x4 *>(&vs[buf][at]) = vreg[u];
+            const uint32_t e = tid + u * THREADS, r = e % TV;
+            const uint32_t at = buf * 2 * KS * TILE + (e / TV) * TILE + (r / (D / 4)) * ROW + (r % (D / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(&lds[at]) = kreg[u];
+            *reinterpret_cast<f32x4 *>(&lds[at + KS * TILE]) = vreg[u];
         }
     };
 
     if (t_begin < tiles) {
-        fetch(t_begin * kTileKeys);
-        stash(t_begin & 1);
+        fetch(t_begin * KN);
+        stash(0, t_begin * KN);
     }
     __syncthreads();
-    for (uint32_t t = t_begin; t < tiles; ++t) {
-        const int buf = t & 1;
+    // step: KS tiles from t0; this wave takes tile t0 + kpart
+    for (uint32_t t0 = t_begin, step = 0; t0 < tiles; t0 += KS, ++step) {
+        const int buf = step & 1;
+        const uint32_t t = t0 + kpart;
         const uint32_t k0 = t * KN;
-        const bool more = t + 1 < tiles;
-        if (more) fetch(k0 + KN);
-        if (wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
+        const bool more = t0 + KS < tiles;
+        if (more) fetch((t0 + KS) * KN);
+        const float *kt = &lds[buf * 2 * KS * TILE + kpart * TILE];   // this wave's K tile
+        const float *vt = kt + KS * TILE;                              // and V tile
+        if (t < tiles && wave_live && !(a.causal && (uint64_t)k0 > wave_last_key)) {
             const bool interior = k0 + KN <= a.kl &&
                                   (!a.causal || (uint64_t)k0 + KN - 1 <= (uint64_t)qw + a.causal_offset);
             // two accumulators (even and odd d pairs) keep two MFMA chains in flight
@@ -872,7 +891,7 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
             for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[h2][r] = 0.0f;
-            const float *krow = &ks[buf][col * ROW + half * QC];
+            const float *krow = kt + col * ROW + half * QC;
 #pragma unroll
             for (int c4 = 0; c4 < QC / 4; ++c4) {
                 const f32x4 kf = *reinterpret_cast<const f32x4 *>(krow + 4 * c4);
@@ -934,16 +953,49 @@ __global__ __launch_bounds__(BM * 2) void sdpa_flash_f32_kernel(const float *__r
             // the VT output tiles are independent chains: issue them side by side
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const float *vrow = &vs[buf][(8 * (j / 4) + 4 * half + j % 4) * ROW + col];
+                const float *vrow = vt + (8 * (j / 4) + 4 * half + j % 4) * ROW + col;
 #pragma unroll
                 for (int tt = 0; tt < VT; ++tt)
                     o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * tt], st[j], o[tt], 0, 0, 0);
             }
         }
-        if (more) stash(buf ^ 1);
+        if (more) stash(buf ^ 1, (t0 + KS) * KN);
         __syncthreads();
     }
     nan_seen = nan_seen || __shfl_xor((int)nan_seen, 32, kWave);
+    if constexpr (KS == 2) {
+        // the two key parts of each query group merged through LDS, as in
+        // the f16 kernel, with natural-exp weights e^(m_s - M)
+        static_assert(QW * (VT * 4 + 1) * kWave * 16 <= sizeof(lds), "merge area");
+        f32x4 *xch = reinterpret_cast<f32x4 *>(&lds[0]) + qgroup * (VT * 4 + 1) * kWave + lane;
+        if (kpart == 1) {
+#pragma unroll
+            for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    xch[(tt * 4 + g) * kWave] =
+                        f32x4{o[tt][4 * g], o[tt][4 * g + 1], o[tt][4 * g + 2], o[tt][4 * g + 3]};
+            xch[VT * 4 * kWave] = f32x4{m, l, nan_seen ? 1.0f : 0.0f, 0.0f};
+        }
+        __syncthreads();
+        if (kpart == 1) return;
+        const f32x4 other = xch[VT * 4 * kWave];
+        const float big = fmaxf(m, other.x);
+        const bool finite = __builtin_isfinite(big);
+        const float w0 = !finite || m == -__builtin_inff() ? 0.0f : expf(m - big);
+        const float w1 = !finite || other.x == -__builtin_inff() ? 0.0f : expf(other.x - big);
+#pragma unroll
+        for (int tt = 0; tt < VT; ++tt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 p = xch[(tt * 4 + g) * kWave];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[tt][4 * g + j] = w0 * o[tt][4 * g + j] + w1 * p[j];
+            }
+        l = w0 * l + w1 * other.y;
+        m = big;
+        nan_seen = nan_seen || other.z != 0.0f;
+    }
     if (!q_live) return;
     if constexpr (kSplit) {
         if (item.parts > 1) {
@@ -1050,6 +1102,22 @@ struct FlashPlan {
 // are several rounds of blocks for the order to balance, they lose: 2048^2
 // D 128 non-causal 95 vs 80, 4096^2 causal 187 vs 167, 4 x 2048^2 causal
 // 220 vs 189.
+// f32: the same in-block split for causal launches of at least one 8-wave
+// block per CU with uneven key ranges (measured below)
+bool key_parts_pay_f32(const k::SdpaShape &sh, bool causal) {
+    const size_t bhs = sh.batch * sh.q_heads;
+    if (!causal || ((sh.q_len + 127) / 128) * bhs < 256) return false;
+    const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
+    const uint32_t offset = kl > ql ? kl - ql : 0, blocks = (ql + 127) / 128;
+    uint64_t total = 0, most = 0;
+    for (uint32_t j = 0; j < blocks; ++j) {
+        const uint64_t t = flash_tiles(ql, kl, true, offset, 128, kFlashN32, j);
+        total += t;
+        most = t > most ? t : most;
+    }
+    return 4 * most * blocks > 5 * total;
+}
+
 bool key_parts_pay(const k::SdpaShape &sh, bool causal) {
     const size_t bhs = sh.batch * sh.q_heads;
     if (!causal || ((sh.q_len + 127) / 128) * bhs < 256 || ((sh.q_len + 255) / 256) * bhs > 256)
@@ -1076,7 +1144,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
-    if (!f32 && key_parts_pay(sh, causal)) {
+    if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
         p.bm = 128;
         p.key_parts = 2;
     } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
@@ -1193,19 +1261,8 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
 
 }  // namespace
 
-// One flash launch for the plan's (D, BM) with the general (mask) / split
-// variant; the f16 kernel also takes its key parts per query group (KS).
-#define ICSDK_FLASH_VARIANTS(KERNEL, D, BM, Q, K, V, M, O)                                         \
-    do {                                                                                           \
-        if (general && split)                                                                      \
-            hipLaunchKernelGGL((KERNEL<D, BM, true, true>), grid, block, 0, s, Q, K, V, M, O, a);  \
-        else if (general)                                                                          \
-            hipLaunchKernelGGL((KERNEL<D, BM, true, false>), grid, block, 0, s, Q, K, V, M, O, a); \
-        else if (split)                                                                            \
-            hipLaunchKernelGGL((KERNEL<D, BM, false, true>), grid, block, 0, s, Q, K, V, M, O, a); \
-        else                                                                                       \
-            hipLaunchKernelGGL((KERNEL<D, BM, false, false>), grid, block, 0, s, Q, K, V, M, O, a);\
-    } while (0)
+// One flash launch for the plan's (D, BM, KS) with the general (mask) /
+// split variant.
 #define ICSDK_FLASH_VARIANTS_KS(KERNEL, D, BM, KS, Q, K, V, M, O)                                  \
     do {                                                                                           \
         if (general && split)                                                                      \
@@ -1222,14 +1279,18 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
 // per SIMD at D 128 and runs with one key part)
 #define ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O)                                         \
     hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a)
-#define ICSDK_FLASH_SHAPES(KERNEL, Q, K, V, M, O)                                                  \
+// the f32 kernel: 64- or 128-query blocks, 128-query blocks with two key
+// parts per query group
+#define ICSDK_FLASH_SHAPES_F32(KERNEL, Q, K, V, M, O)                                              \
     do {                                                                                           \
         if (shape.head_dim == 64) {                                                                \
-            if (plan.bm == 128) ICSDK_FLASH_VARIANTS(KERNEL, 64, 128, Q, K, V, M, O);              \
-            else ICSDK_FLASH_VARIANTS(KERNEL, 64, 64, Q, K, V, M, O);                              \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 64, Q, K, V, M, O);                      \
+            else if (plan.bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 128, 1, Q, K, V, M, O);   \
+            else ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 64, 1, Q, K, V, M, O);                        \
         } else {                                                                                   \
-            if (plan.bm == 128) ICSDK_FLASH_VARIANTS(KERNEL, 128, 128, Q, K, V, M, O);             \
-            else ICSDK_FLASH_VARIANTS(KERNEL, 128, 64, Q, K, V, M, O);                             \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 128, Q, K, V, M, O);                     \
+            else if (plan.bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 128, 1, Q, K, V, M, O);  \
+            else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
         }                                                                                          \
     } while (0)
 // the f16 kernel: 64-, 128- or 256-query blocks, 128-query blocks with two
@@ -1266,8 +1327,9 @@ hipError_t sdpa_f32(const float *q, const float *k, const float *v, const float 
     const SdpaArgs a = flash_args(plan, shape, scale, causal, workspace);
     const bool split = plan.max_parts > 1;
     const bool general = mask != nullptr;
-    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm);
-    ICSDK_FLASH_SHAPES(sdpa_flash_f32_kernel, q, k, v, mask, out);
+    const uint32_t ks = general ? 1 : plan.key_parts;
+    const dim3 grid((unsigned)(shape.batch * shape.q_heads * plan.items)), block(2 * plan.bm * ks);
+    ICSDK_FLASH_SHAPES_F32(sdpa_flash_f32_kernel, q, k, v, mask, out);
     const hipError_t status = hipGetLastError();
     return status != hipSuccess || !split ? status : combine_splits(a, plan, out, s);
 }
@@ -1296,10 +1358,9 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
 }  // namespace k
 
 #undef ICSDK_FLASH_SHAPES_F16
-#undef ICSDK_FLASH_SHAPES
+#undef ICSDK_FLASH_SHAPES_F32
 #undef ICSDK_FLASH_VARIANTS_KS2
 #undef ICSDK_FLASH_VARIANTS_KS
-#undef ICSDK_FLASH_VARIANTS
 
 
 }  // namespace icsdk

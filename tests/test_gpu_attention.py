@@ -266,10 +266,11 @@ def test_split_key_range_special_rows(sdk, orc, dtype):
     check(got[0, 0, 3:], want[0, 0, 3:], weight[0, 0, 3:], dtype, "ordinary row")
 
 
-# f16 causal shapes whose 256-query blocks would be about one round on the
-# GPU with uneven key ranges: blocks of 128 queries whose 8 waves take 4
-# query groups x 2 key parts (alternate 64-key tiles), merged in LDS.
-# The oracle runs on the first and the last kv head's query heads only.
+# Causal shapes with uneven key ranges that take blocks of 128 queries whose
+# 8 waves are 4 query groups x 2 key parts (alternate key tiles: 64 keys
+# f16, 32 f32), merged in LDS: f16 where its 256-query blocks would be about
+# one round on the GPU, f32 from 256 such blocks. The oracle runs on the
+# first and the last kv head's query heads only.
 KEY_PART_SHAPES = [
     (1, 128, 16, 512, 512, 64, 64),     # 4 and 8 key tiles per 256 queries
     (2, 64, 16, 512, 512, 128, 128),    # batch 2, D 128
@@ -288,46 +289,50 @@ def head_subset(q, k, v, got):
 
 
 @pytest.mark.parametrize("shape", KEY_PART_SHAPES)
-def test_key_parts(sdk, orc, shape):
-    q, k, v, _ = inputs(orc, shape, "f16", 34, False)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_key_parts(sdk, orc, shape, dtype):
+    q, k, v, _ = inputs(orc, shape, dtype, 34, False)
     scale = 1.0 / np.sqrt(shape[5])
-    got = run_device(sdk, q, k, v, None, scale, True, "f16")
+    got = run_device(sdk, q, k, v, None, scale, True, dtype)
     q, k, v, got = head_subset(q, k, v, got)
     want = orc.sdpa(q, k, v, None, scale, True)
     weight = orc.sdpa_abs_weight(q, k, v, None, scale, True)
-    check(got, want, weight, "f16", f"{shape} causal")
+    check(got, want, weight, dtype, f"{shape} causal")
 
 
 @pytest.mark.parametrize("direction", [1.0, -1.0])
-def test_key_parts_growing_row_maxima(sdk, orc, direction):
-    """Scores climbing (or falling) 60 log2 units along the keys: the two
-    key parts' running maxima move at different tiles and are merged with
-    their own weights."""
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_key_parts_growing_row_maxima(sdk, orc, direction, dtype):
+    """Scores climbing (or falling) along the keys (60 log2 units for f16,
+    20 for f32, as in test_growing_row_maxima): the two key parts' running
+    maxima move at different tiles and are merged with their own weights."""
     shape = (1, 128, 16, 512, 512, 64, 64)
-    q, k, v, _ = inputs(orc, shape, "f16", 35, False)
+    q, k, v, _ = inputs(orc, shape, dtype, 35, False)
     scale = 1.0 / np.sqrt(shape[5])
-    reach = 60.0 / (4.0 * scale * np.log2(np.e))
+    climb = 60.0 if dtype == "f16" else 20.0
+    reach = climb / (4.0 * scale * np.log2(np.e))
     q[..., 0] = 4.0
     k[..., :, 0] = (direction * reach * np.arange(shape[4]) / shape[4]).astype(k.dtype)
-    got = run_device(sdk, q, k, v, None, scale, True, "f16")
+    got = run_device(sdk, q, k, v, None, scale, True, dtype)
     q, k, v, got = head_subset(q, k, v, got)
     want = orc.sdpa(q, k, v, None, scale, True)
     weight = orc.sdpa_abs_weight(q, k, v, None, scale, True)
-    check(got, want, weight, "f16", f"direction={direction}")
+    check(got, want, weight, dtype, f"direction={direction}")
 
 
-def test_key_parts_special_rows(sdk, orc):
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_key_parts_special_rows(sdk, orc, dtype):
     """Special rows across the two key parts, bitwise vs the oracle: a NaN
     query (every score NaN: zero row); a NaN key in the second part's first
     tile (rows that see it are NaN); a +inf key component in the second
     part's second tile (rows that see it with a positive query component:
     max +inf, zero row; negative: -inf score, the key drops out)."""
     shape = (1, 128, 16, 512, 512, 64, 64)
-    q, k, v, _ = inputs(orc, shape, "f16", 36, False)
+    q, k, v, _ = inputs(orc, shape, dtype, 36, False)
     q[0, 0, 1, 5] = np.nan
     k[0, 15, 70, 3] = np.nan
     k[0, 15, 200, 0] = np.inf
-    got = run_device(sdk, q, k, v, None, 0.125, True, "f16")
+    got = run_device(sdk, q, k, v, None, 0.125, True, dtype)
     q, k, v, got = head_subset(q, k, v, got)
     want = orc.sdpa(q, k, v, None, 0.125, True)
     assert np.array_equal(np.isnan(got), np.isnan(want))
@@ -337,4 +342,4 @@ def test_key_parts_special_rows(sdk, orc):
     weight = orc.sdpa_abs_weight(q, k, v, None, 0.125, True)
     live = ~zero & ~np.isnan(want).any(axis=-1)
     assert live[0, -1, :70].all()
-    check(got[live], want[live], weight[live], "f16", "ordinary rows")
+    check(got[live], want[live], weight[live], dtype, "ordinary rows")
