@@ -1144,7 +1144,15 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         return p;
     p.flash = true;
     const size_t bhs = sh.batch * sh.q_heads;
+    // f16 grids of 64-255 blocks of 128 queries (fewer blocks than CUs)
+    // also take two key parts, with the key-range split across blocks kept:
+    // twice the waves per block (12 heads x 1024^2 D 64: 18.7 -> 16.9 us)
+    const uint64_t q128 = ((sh.q_len + 127) / 128) * bhs;
+    const bool small_grid = !f32 && q128 >= 64 && q128 < 256;
     if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
+        p.bm = 128;
+        p.key_parts = 2;
+    } else if (small_grid) {
         p.bm = 128;
         p.key_parts = 2;
     } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
@@ -1159,7 +1167,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0;
     auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
-    if (split && p.key_parts == 1) {
+    if (split && (p.key_parts == 1 || small_grid)) {
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
@@ -1274,11 +1282,15 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             hipLaunchKernelGGL((KERNEL<D, BM, false, false, KS>), grid, block, 0, s, Q, K, V, M, O, a);\
     } while (0)
-// two key parts: the raw-product, unsplit variant only (a plan with two key
-// parts splits no query block; the general variant would not fit two waves
-// per SIMD at D 128 and runs with one key part)
+// two key parts: the raw-product variants only (the general variant would
+// not fit two waves per SIMD at D 128 and runs with one key part)
 #define ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O)                                         \
-    hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a)
+    do {                                                                                           \
+        if (split)                                                                                 \
+            hipLaunchKernelGGL((KERNEL<D, 128, false, true, 2>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else                                                                                       \
+            hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a);\
+    } while (0)
 // the f32 kernel: 64- or 128-query blocks, 128-query blocks with two key
 // parts per query group
 #define ICSDK_FLASH_SHAPES_F32(KERNEL, Q, K, V, M, O)                                              \

@@ -343,3 +343,42 @@ def test_key_parts_special_rows(sdk, orc, dtype):
     live = ~zero & ~np.isnan(want).any(axis=-1)
     assert live[0, -1, :70].all()
     check(got[live], want[live], weight[live], dtype, "ordinary rows")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("scale", [0.125, -0.125])
+def test_key_part_plan_general_variant(sdk, orc, dtype, scale):
+    """A mask (or a scale <= 0) on a shape whose plan takes two key parts:
+    the general variant runs with one key part on the same 128-query plan."""
+    shape = (1, 128, 16, 512, 512, 64, 64)
+    q, k, v, mask = inputs(orc, shape, dtype, 37, scale > 0)
+    got = run_device(sdk, q, k, v, mask, scale, True, dtype)
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, mask, scale, True)
+    weight = orc.sdpa_abs_weight(q, k, v, mask, scale, True)
+    check(got, want, weight, dtype, f"scale={scale} mask={mask is not None}")
+
+
+def test_small_grid_key_parts_special_rows(sdk, orc):
+    """f16, 64 blocks of 128 queries: two key parts per query group and the
+    key range split over blocks (merged by the combine kernel). Special rows
+    bitwise vs the oracle across both merges: a NaN query (zero row), a NaN
+    key in the second half of the range (every row NaN), and a +inf key
+    component in the first half (rows with a positive query component:
+    max +inf, zero row)."""
+    shape = (1, 64, 16, 128, 1024, 64, 64)
+    q, k, v, _ = inputs(orc, shape, "f16", 38, False)
+    q[0, 0, 1, 5] = np.nan
+    k[0, 15, 900, 3] = np.nan
+    k[0, 0, 70, 0] = np.inf
+    got = run_device(sdk, q, k, v, None, 0.125, False, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, 0.125, False)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    zero = (want == 0).all(axis=-1)
+    assert zero[0, 0, 1] and zero[0, 1].any() and np.isnan(want[0, -1]).all()
+    assert (got[zero] == 0).all()
+    weight = orc.sdpa_abs_weight(q, k, v, None, 0.125, False)
+    live = ~zero & ~np.isnan(want).any(axis=-1)
+    assert live.any()
+    check(got[live], want[live], weight[live], "f16", "ordinary rows")
