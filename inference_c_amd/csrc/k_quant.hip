@@ -372,19 +372,22 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
     auto fetch_w = [&](uint32_t c0) {
         const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
         const uint8_t *base = tile + (uint64_t)c0 * kBytes - 16;
-        // Ordinary (L2-allocating) loads: a row's 544-byte chunks are not
-        // line-aligned, so the line holding a chunk boundary is read by two
-        // consecutive chunks; with non-temporal loads L2 let it go in between
-        // and it came from HBM twice (1.13 x the packed bytes at 4 rows,
-        // 1.004 x with these; 16 rows 59.0 -> 56.4 us).
+        // Non-temporal loads. A row's 544-byte chunks are not line-aligned,
+        // so the line holding a chunk boundary is read by two consecutive
+        // chunks and, not kept in L2 in between, comes from HBM twice (1.13 x
+        // the packed bytes at 4 rows). L2-allocating loads read it once, but
+        // after other traffic has left the last-level cache dirty (a 600 MB
+        // write just before) the launch took 95 us instead of 48: the
+        // weights then evict that data. Back to back they gained nothing.
         if (nb == kChunk) {
 #pragma unroll
             for (int i = 0; i < (int)kPasses; ++i)
-                seg[i] = *reinterpret_cast<const u32x4 *>(base + off_full[i]);
+                seg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off_full[i]));
         } else {
 #pragma unroll
             for (int i = 0; i < (int)kPasses; ++i)
-                seg[i] = *reinterpret_cast<const u32x4 *>(base + seg_off(lane + kWave * i, nb));
+                seg[i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(base + seg_off(lane + kWave * i, nb)));
         }
     };
 
