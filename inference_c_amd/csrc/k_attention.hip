@@ -1109,13 +1109,18 @@ bool key_parts_pay_f32(const k::SdpaShape &sh, bool causal) {
     if (!causal || ((sh.q_len + 127) / 128) * bhs < 256) return false;
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0, blocks = (ql + 127) / 128;
-    uint64_t total = 0, most = 0;
-    for (uint32_t j = 0; j < blocks; ++j) {
+    // every block up to 1024 of them, else an even sample (the longest,
+    // the last block, always in it)
+    const uint32_t stride = blocks > 1024 ? blocks / 1024 : 1;
+    uint64_t total = 0, most = 0, n = 0;
+    for (uint32_t j = blocks - 1;; j -= stride) {
         const uint64_t t = flash_tiles(ql, kl, true, offset, 128, kFlashN32, j);
         total += t;
         most = t > most ? t : most;
+        ++n;
+        if (j < stride) break;
     }
-    return 4 * most * blocks > 5 * total;
+    return 4 * most * n > 5 * total;
 }
 
 bool key_parts_pay(const k::SdpaShape &sh, bool causal) {
