@@ -9,7 +9,11 @@
 // quant_gemv_kernel (one or two input rows) and quant_mma_kernel (three or more):
 // y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
 //
-// GEMV: a wave owns O output rows and walks them in chunks of 64 blocks.
+// GEMV: a wave works on O output rows in chunks of 64 blocks -- with one
+// input row the block's 4 waves share O rows and take every 4th chunk
+// (their sums meet in LDS: four short waves per block instead of one long
+// one, so a launch has no long last round), with two each wave owns O rows
+// and walks all their chunks.
 // Each chunk of each row is a contiguous byte range; the wave reads it with
 // coalesced 16-byte loads (the aligned 16-byte segments covering the range)
 // into its own LDS region, then lane l takes block l of the chunk from LDS:
@@ -20,8 +24,9 @@
 // both re-aligns it and turns it into two exact f16 subnormals, multiplied
 // with the x pairs by v_dot2_f32_f16 in f32 (gemv_block below); x for the
 // lane's block is loaded once per chunk and reused for all O rows. The
-// wave's partial sums are folded with DPP at the end. Bound: HBM bytes of
-// the packed weights (1.0625 or 0.5625 bytes per weight).
+// wave's partial sums (kept as 2^-24 times the dot products, the value
+// offset's share starting each block's sum) are folded with DPP at the end.
+// Bound: HBM bytes of the packed weights (1.0625 or 0.5625 bytes per weight).
 #include "kern_common.hpp"
 #include "kernels.hpp"
 
@@ -74,22 +79,30 @@ struct GemvSel {
           s(sh ? 0x0c0c0302u : 0x0c0c0100u) {}
 };
 
-// sum_k x_k w_k of one block (f32) for each of R input rows, and the
-// block's scale; x[r] holds row r's 32 f16 of the block as 16 pairs, xsum[r]
-// their sum. The weights are decoded once for the R rows.
+// v_dot2_f32_f16 d = a.lo * b.lo + a.hi * b.hi + c with c in its own
+// register (the compiler's accumulate-in-place form needs a copy of c per
+// chain when c is shared)
+__device__ inline float dot2_from(half2_t a, half2_t b, float c) {
+    float d;
+    asm volatile("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// 2^-24 * sum_k x_k w_k of one block (f32) for each of R input rows, and
+// the block's scale (f16 bits in the low half); x[r] holds row r's 32 f16
+// of the block as 16 pairs, base[r] = -offset * 2^-24 * (their sum), the
+// value offset's share. The weights are decoded once for the R rows.
 template <bool kQ8, int R>
 __device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const GemvSel &sel,
-                                  const uint32_t (&x)[R][16], const float (&xsum)[R], float &scale,
+                                  const uint32_t (&x)[R][16], const float (&base)[R], uint32_t &scale,
                                   float (&dot)[R]) {
     constexpr int W = GemvFmt<kQ8>::kWin;
     const uint32_t *words = reinterpret_cast<const uint32_t *>(chunk + (off & ~3u));
     uint32_t e[W];
 #pragma unroll
     for (int i = 0; i < W; ++i) e[i] = words[i];
-    scale = (float)__builtin_bit_cast(_Float16, (uint16_t)__builtin_amdgcn_perm(e[0], e[0], sel.s));
+    scale = __builtin_amdgcn_perm(e[0], e[0], sel.s);
     float s0[R], s1[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) s0[r] = s1[r] = 0.0f;
     if constexpr (kQ8) {
 #pragma unroll
         for (int i = 0; i < W; ++i) e[i] ^= 0x80808080u;
@@ -99,16 +112,19 @@ __device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const Gemv
             const half2_t pb = as_half2(__builtin_amdgcn_perm(e[m + 1], e[m], sel.b));
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                s0[r] = __builtin_amdgcn_fdot2(pa, as_half2(x[r][2 * m]), s0[r], false);
-                s1[r] = __builtin_amdgcn_fdot2(pb, as_half2(x[r][2 * m + 1]), s1[r], false);
+                if (m == 0) {
+                    s0[r] = dot2_from(pa, as_half2(x[r][0]), base[r]);
+                    s1[r] = dot2_from(pb, as_half2(x[r][1]), 0.0f);
+                } else {
+                    s0[r] = __builtin_amdgcn_fdot2(pa, as_half2(x[r][2 * m]), s0[r], false);
+                    s1[r] = __builtin_amdgcn_fdot2(pb, as_half2(x[r][2 * m + 1]), s1[r], false);
+                }
             }
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) dot[r] = __builtin_fmaf(s0[r] + s1[r], 16777216.0f, -128.0f * xsum[r]);
+        for (int r = 0; r < R; ++r) dot[r] = s0[r] + s1[r];
     } else {
-        float h0[R], h1[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) h0[r] = h1[r] = 0.0f;
+        // s: low nibbles (weight k at k), h: high nibbles (weight k at 16 k)
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t pa = __builtin_amdgcn_perm(e[m + 1], e[m], sel.a);
@@ -117,22 +133,25 @@ __device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const Gemv
             const half2_t ha = as_half2(pa & 0x00f000f0u), hb = as_half2(pb & 0x00f000f0u);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                s0[r] = __builtin_amdgcn_fdot2(la, as_half2(x[r][2 * m]), s0[r], false);
-                s1[r] = __builtin_amdgcn_fdot2(lb, as_half2(x[r][2 * m + 1]), s1[r], false);
-                h0[r] = __builtin_amdgcn_fdot2(ha, as_half2(x[r][8 + 2 * m]), h0[r], false);
-                h1[r] = __builtin_amdgcn_fdot2(hb, as_half2(x[r][8 + 2 * m + 1]), h1[r], false);
+                if (m == 0) {
+                    s0[r] = dot2_from(la, as_half2(x[r][0]), base[r]);
+                    s1[r] = dot2_from(ha, as_half2(x[r][8]), 0.0f);
+                } else {
+                    s0[r] = __builtin_amdgcn_fdot2(la, as_half2(x[r][2 * m]), s0[r], false);
+                    s1[r] = __builtin_amdgcn_fdot2(ha, as_half2(x[r][8 + 2 * m]), s1[r], false);
+                }
+                s0[r] = __builtin_amdgcn_fdot2(lb, as_half2(x[r][2 * m + 1]), s0[r], false);
+                s1[r] = __builtin_amdgcn_fdot2(hb, as_half2(x[r][8 + 2 * m + 1]), s1[r], false);
             }
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            dot[r] = __builtin_fmaf(__builtin_fmaf(h0[r] + h1[r], 0.0625f, s0[r] + s1[r]), 16777216.0f,
-                                    -8.0f * xsum[r]);
+        for (int r = 0; r < R; ++r) dot[r] = __builtin_fmaf(s1[r], 0.0625f, s0[r]);
     }
 }
 
 // Grid: x = waves of O output rows (4 waves per block), y = groups of R
 // input rows. Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
-template <bool kQ8, int R, int O>
+template <bool kQ8, int R, int O, bool kSplit>
 __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__restrict__ x,
                                                             const uint8_t *__restrict__ w,
                                                             uint16_t *__restrict__ y,
@@ -144,10 +163,15 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
     __shared__ __attribute__((aligned(16))) uint8_t stage[kBlock / kWave][O][kVecs * 16];
     const uint32_t lane = threadIdx.x & (kWave - 1);
     uint8_t (*region)[kVecs * 16] = stage[threadIdx.x / kWave];
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(
-        (blockIdx.x * kBlock + threadIdx.x) / kWave);
-    const uint32_t o0 = wave * O;
-    if (o0 >= out) return;
+    // kSplit: the block's 4 waves share its O output rows and take every
+    // 4th chunk of 64 blocks (wave k: chunks k, k + 4, ...), their sums
+    // meeting in LDS; else each wave owns O rows and walks all their chunks
+    constexpr uint32_t kWaves = kBlock / kWave;
+    constexpr uint32_t kParts = kSplit ? kWaves : 1;
+    const uint32_t wib = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t kpart = kSplit ? wib : 0;
+    const uint32_t o0 = (kSplit ? blockIdx.x : blockIdx.x * kWaves + wib) * O;
+    if (o0 >= out) return;   // with kSplit the whole block
     const uint32_t r0 = blockIdx.y * R;
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
@@ -170,8 +194,8 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
     const uint8_t *tile = w + row_of(0) * row_bytes;
     // lane l's selectors: its block's alignment is the row's lead parity
     // flipped on odd lanes (kBytes is 2 mod 4), so two sets serve every row.
-    // (A lane past a partial chunk's end reads block nb - 1 with them:
-    // garbage, discarded.)
+    // (A lane past a partial chunk's end reads its own block's place in the
+    // region with them: stale words, decoded to finite values, discarded.)
     const GemvSel sel_lead0((kBytes * lane) & 2u), sel_lead2((2 + kBytes * lane) & 2u);
 
     float acc[O][R];
@@ -180,7 +204,7 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[o][r] = 0.0f;
 
-    for (uint32_t c0 = 0; c0 < blocks; c0 += kWave) {
+    for (uint32_t c0 = kpart * kWave; c0 < blocks; c0 += kParts * kWave) {
         const uint32_t nb = min((uint32_t)kWave, blocks - c0);
         // the aligned 16-byte segments holding this chunk of each row; a
         // segment never crosses a page, so the bytes around the chunk that
@@ -203,7 +227,7 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         }
         const uint32_t b = c0 + min(lane, nb - 1);
         uint32_t xv[R][16];
-        float xsum[R];
+        float base[R];   // -offset * 2^-24 * (the x sum of the lane's block)
         const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -222,7 +246,8 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
                 xs0 = __builtin_amdgcn_fdot2(as_half2(xv[r][i]), one2, xs0, false);
                 xs1 = __builtin_amdgcn_fdot2(as_half2(xv[r][i + 1]), one2, xs1, false);
             }
-            xsum[r] = xs0 + xs1;
+            // -offset * 2^-24 * sum (exact: a power of two times the sum)
+            base[r] = (xs0 + xs1) * (kQ8 ? -0x1p-17f : -0x1p-21f);
         }
 #pragma unroll
         for (int o = 0; o < O; ++o)
@@ -238,27 +263,51 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         const bool live = lane < nb;
 #pragma unroll
         for (int o = 0; o < O; ++o) {
-            const uint32_t off = lead[o] + (b - c0) * kBytes;
-            float scale, dot[R];
-            gemv_block<kQ8, R>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0, xv, xsum, scale,
+            // lane l's block, also past a partial chunk's end (inside the
+            // region: its words are stale, decoded to finite values)
+            const uint32_t off = lead[o] + lane * kBytes;
+            uint32_t scale;
+            float dot[R];
+            gemv_block<kQ8, R>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0, xv, base, scale,
                                dot);
-            // a lane past the chunk's end adds 0 * (a finite dot): its scale
-            // bytes may be anything, its decoded values are subnormals
-            const float sc = live ? scale : 0.0f;
+            // a lane past the chunk's end adds 0 * (a finite dot)
+            const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(live ? scale : 0u));
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[o][r] = __builtin_fmaf(sc, dot[r], acc[o][r]);
+            for (int r = 0; r < R; ++r) acc[o][r] = __builtin_fmaf((float)sc, dot[r], acc[o][r]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
+    // sums are kept as 2^-24 times the dot products until here (exact)
+    if constexpr (kSplit) {
+        __shared__ float part[kWaves][O * R];
 #pragma unroll
-    for (int o = 0; o < O; ++o)
+        for (int o = 0; o < O; ++o)
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float total = wave_sum(acc[o][r]);
-            if (lane == 0 && o0 + o < out && r0 + r < rows)
-                y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+            for (int r = 0; r < R; ++r) {
+                const float total = wave_sum(acc[o][r]);
+                if (lane == 0) part[kpart][o * R + r] = total;
+            }
+        __syncthreads();
+        if (threadIdx.x < O * R) {
+            const uint32_t o = threadIdx.x / R, r = threadIdx.x % R;
+            float total = 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < kWaves; ++k) total += part[k][threadIdx.x];
+            if (o0 + o < out && r0 + r < rows)
+                y[(uint64_t)(r0 + r) * out + o0 + o] =
+                    __builtin_bit_cast(uint16_t, (_Float16)(total * 0x1p24f));
         }
+    } else {
+#pragma unroll
+        for (int o = 0; o < O; ++o)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float total = wave_sum(acc[o][r]) * 0x1p24f;
+                if (lane == 0 && o0 + o < out && r0 + r < rows)
+                    y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+            }
+    }
 }
 
 // quant_mma_kernel (16 input rows per block row): each 32-weight block of 16
@@ -616,15 +665,14 @@ __global__ __launch_bounds__(kBlock) void quantize_kernel(const uint16_t *__rest
     }
 }
 
-template <bool kQ8, int R, int O>
+template <bool kQ8, int R, int O, bool kSplit>
 hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
                        size_t in, size_t out, hipStream_t s) {
-    constexpr uint32_t kWavesPerBlock = kBlock / kWave;
-    const size_t waves = (out + O - 1) / O;
-    const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock),
+    const size_t rows_per_block = kSplit ? O : O * (kBlock / kWave);
+    const dim3 grid((unsigned)((out + rows_per_block - 1) / rows_per_block),
                     (unsigned)((rows + R - 1) / R));
-    quant_gemv_kernel<kQ8, R, O><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                         (uint32_t)out);
+    quant_gemv_kernel<kQ8, R, O, kSplit><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows,
+                                                                 (uint32_t)in, (uint32_t)out);
     return hipGetLastError();
 }
 
@@ -653,8 +701,9 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
                                                                               (uint32_t)out);
         return hipGetLastError();
     }
-    // One or two input rows: the GEMV, 4 output rows per wave (2, 6 and 8
-    // measured slower for both formats), decoding each weight once for the
+    // One or two input rows: the GEMV, 4 output rows per wave, or per block
+    // of 4 waves splitting the chunks for one row (2, 6 and 8 measured
+    // slower for both formats and both forms), decoding each weight once for the
     // rows. From three rows quant_mma_kernel, which decodes each weight once
     // for up to 16 ([28672, 8192] Q8_0: 2 rows 51 us GEMV vs 56 MFMA; 4 rows
     // 64 vs 52; Q4_0 2 rows 39 vs 44, 4 rows 52 vs 40). Its 32-bit offsets
@@ -671,10 +720,10 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
             status = launch_mma<kQ8>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else if (left == 2) {
             done = 2;
-            status = launch_gemv<kQ8, 2, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+            status = launch_gemv<kQ8, 2, 4, false>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else {
             done = left < kMaxGroups ? left : kMaxGroups;
-            status = launch_gemv<kQ8, 1, 4>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+            status = launch_gemv<kQ8, 1, 4, true>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         }
         if (status != hipSuccess) return status;
         r0 += done;
