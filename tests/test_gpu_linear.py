@@ -302,6 +302,9 @@ QUANT_SHAPES = [  # rows, in, out
     (1, 32, 1), (1, 64, 7), (1, 2048, 256), (2, 4096, 130), (3, 96, 33), (4, 1024, 64),
     (5, 512, 40), (8, 256, 16), (17, 2080, 24), (64, 768, 96), (1, 8192, 512),
     (6, 8192, 100), (33, 544, 50),
+    # one row: a block's 4 waves split the 64-block chunks -- wave 1 with a
+    # partial chunk; 6 chunks, so waves 0 and 1 take two (the second partial)
+    (1, 2112, 5), (1, 10336, 9),
     # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
