@@ -1151,14 +1151,22 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const size_t bhs = sh.batch * sh.q_heads;
     // f16 grids of 64-255 blocks of 128 queries (fewer blocks than CUs)
     // also take two key parts, with the key-range split across blocks kept:
-    // twice the waves per block (12 heads x 1024^2 D 64: 18.7 -> 16.9 us)
+    // twice the waves per block (12 heads x 1024^2 D 64: 18.7 -> 16.9 us).
+    // Non-causal ones of at most 128 such blocks over at most 1024 keys take
+    // 64-query blocks (4 waves: 2 query groups x 2 key parts) and no split:
+    // at most one block per CU, no merge launch (us, same box: 12 heads x
+    // 1024^2 D 64 17.4 -> 14.3, D 128 25.9 -> 20.8, 32 heads x 512^2 D 64
+    // 11.2 -> 9.6, 8 heads x 1024^2 D 64 15.7 -> 13.8); over 2048 keys, or
+    // with more blocks than CUs, the split plan stays faster (4 heads x
+    // 2048^2 D 128 31.7 vs 35.7; 20 heads x 1024^2 D 64 17.0 vs 25.9).
     const uint64_t q128 = ((sh.q_len + 127) / 128) * bhs;
     const bool small_grid = !f32 && q128 >= 64 && q128 < 256;
+    const bool small_short = small_grid && !causal && q128 <= 128 && sh.kv_len <= 1024;
     if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
         p.bm = 128;
         p.key_parts = 2;
     } else if (small_grid) {
-        p.bm = 128;
+        p.bm = small_short ? 64 : 128;
         p.key_parts = 2;
     } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
     else if (((sh.q_len + 127) / 128) * bhs >= 64) p.bm = 128;
@@ -1172,7 +1180,9 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0;
     auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
-    if (split && (p.key_parts == 1 || small_grid)) {
+    // (64-query blocks with two key parts are never split: the kernel has
+    // no split instance of them)
+    if (split && (p.key_parts == 1 || (small_grid && !small_short))) {
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
@@ -1296,6 +1306,14 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a);\
     } while (0)
+// f16 two-part blocks: also 64-query blocks (unsplit by construction)
+#define ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, D, Q, K, V, M, O)                                     \
+    do {                                                                                           \
+        if (plan.bm == 64)                                                                         \
+            hipLaunchKernelGGL((KERNEL<D, 64, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else                                                                                       \
+            ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O);                                    \
+    } while (0)
 // the f32 kernel: 64- or 128-query blocks, 128-query blocks with two key
 // parts per query group
 #define ICSDK_FLASH_SHAPES_F32(KERNEL, Q, K, V, M, O)                                              \
@@ -1310,18 +1328,18 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
         }                                                                                          \
     } while (0)
-// the f16 kernel: 64-, 128- or 256-query blocks, 128-query blocks with two
-// key parts per query group
+// the f16 kernel: 64-, 128- or 256-query blocks, 64- or 128-query blocks
+// with two key parts per query group
 #define ICSDK_FLASH_SHAPES_F16(KERNEL, Q, K, V, M, O)                                              \
     do {                                                                                           \
         const int bm = (int)plan.bm;                                                               \
         if (shape.head_dim == 64) {                                                                \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 64, Q, K, V, M, O);                      \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, 64, Q, K, V, M, O);                      \
             else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 256, 1, Q, K, V, M, O);        \
             else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 128, 1, Q, K, V, M, O);        \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 64, 1, Q, K, V, M, O);                        \
         } else {                                                                                   \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 128, Q, K, V, M, O);                     \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, 128, Q, K, V, M, O);                     \
             else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 256, 1, Q, K, V, M, O);       \
             else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 128, 1, Q, K, V, M, O);       \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
@@ -1376,6 +1394,7 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
 
 #undef ICSDK_FLASH_SHAPES_F16
 #undef ICSDK_FLASH_SHAPES_F32
+#undef ICSDK_FLASH_VARIANTS_KS2_F16
 #undef ICSDK_FLASH_VARIANTS_KS2
 #undef ICSDK_FLASH_VARIANTS_KS
 

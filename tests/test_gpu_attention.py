@@ -36,7 +36,7 @@ SHAPES = [  # batch, q heads, kv heads, q len, kv len, head dim, value dim
     (1, 2, 2, 600, 600, 64, 64),    # MFMA path, causal: long query blocks split, short ones whole
     (1, 64, 8, 130, 150, 64, 64),   # 128-query blocks (>= 64 of them): ragged query and key tiles
     (1, 32, 4, 256, 300, 128, 128), # 128-query blocks at D 128, 8 q-heads per kv head
-    (1, 64, 16, 128, 1024, 64, 64), # 128-query blocks with split key ranges
+    (1, 64, 16, 128, 1024, 64, 64), # causal: 128-query blocks, split key ranges; else 64-query two-part blocks
     (2, 64, 8, 257, 100, 64, 64),   # f16 256-query blocks (>= 256 of them), ragged; f32 128
     (1, 128, 32, 300, 90, 128, 128),  # f16 256-query blocks at D 128
 ]
@@ -360,17 +360,66 @@ def test_key_part_plan_general_variant(sdk, orc, dtype, scale):
 
 
 def test_small_grid_key_parts_special_rows(sdk, orc):
-    """f16, 64 blocks of 128 queries: two key parts per query group and the
-    key range split over blocks (merged by the combine kernel). Special rows
-    bitwise vs the oracle across both merges: a NaN query (zero row), a NaN
-    key in the second half of the range (every row NaN), and a +inf key
-    component in the first half (rows with a positive query component:
-    max +inf, zero row)."""
-    shape = (1, 64, 16, 128, 1024, 64, 64)
+    """f16, 64 blocks of 128 queries over 1536 keys: two key parts per query
+    group and the key range split over blocks (merged by the combine
+    kernel). Special rows bitwise vs the oracle across both merges: a NaN
+    query (zero row), a NaN key in the second half of the range (every row
+    NaN), and a +inf key component in the first half (rows with a positive
+    query component: max +inf, zero row)."""
+    shape = (1, 64, 16, 128, 1536, 64, 64)
     q, k, v, _ = inputs(orc, shape, "f16", 38, False)
     q[0, 0, 1, 5] = np.nan
-    k[0, 15, 900, 3] = np.nan
+    k[0, 15, 1300, 3] = np.nan
     k[0, 0, 70, 0] = np.inf
+    got = run_device(sdk, q, k, v, None, 0.125, False, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, 0.125, False)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    zero = (want == 0).all(axis=-1)
+    assert zero[0, 0, 1] and zero[0, 1].any() and np.isnan(want[0, -1]).all()
+    assert (got[zero] == 0).all()
+    weight = orc.sdpa_abs_weight(q, k, v, None, 0.125, False)
+    live = ~zero & ~np.isnan(want).any(axis=-1)
+    assert live.any()
+    check(got[live], want[live], weight[live], "f16", "ordinary rows")
+
+
+# f16, non-causal, 64-128 blocks of 128 queries over at most 1024 keys:
+# 64-query blocks of 4 waves (2 query groups x 2 key parts, merged in LDS),
+# no key-range split; with a mask the general variant runs one key part on
+# the same 64-query plan.
+SHORT_GRID_SHAPES = [
+    (1, 64, 16, 128, 1024, 64, 64),     # 64 blocks of 128 queries
+    (1, 12, 12, 1024, 1024, 64, 64),    # 96, one q head per kv head
+    (1, 96, 24, 100, 1000, 128, 128),   # D 128, ragged queries and keys
+    (2, 32, 8, 200, 512, 64, 64),       # batch 2, 128 blocks, a ragged 64-query block
+    (1, 64, 64, 130, 77, 128, 128),     # two key tiles, the second ragged
+]
+
+
+@pytest.mark.parametrize("shape", SHORT_GRID_SHAPES)
+@pytest.mark.parametrize("masked", [False, True])
+def test_short_small_grid(sdk, orc, shape, masked):
+    q, k, v, mask = inputs(orc, shape, "f16", 39, masked)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, mask, scale, False, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, mask, scale, False)
+    weight = orc.sdpa_abs_weight(q, k, v, mask, scale, False)
+    check(got, want, weight, "f16", f"{shape} mask={masked}")
+
+
+def test_short_small_grid_special_rows(sdk, orc):
+    """The 64-query two-part plan, special rows bitwise vs the oracle: a NaN
+    query (zero row), a NaN key in the second key part's first tile (every
+    row of that kv head NaN), a +inf key component in the first part's
+    second tile (rows with a positive query component: max +inf, zero
+    row)."""
+    shape = (1, 64, 16, 128, 1024, 64, 64)
+    q, k, v, _ = inputs(orc, shape, "f16", 40, False)
+    q[0, 0, 1, 5] = np.nan
+    k[0, 15, 70, 3] = np.nan
+    k[0, 0, 130, 0] = np.inf
     got = run_device(sdk, q, k, v, None, 0.125, False, "f16")
     q, k, v, got = head_subset(q, k, v, got)
     want = orc.sdpa(q, k, v, None, 0.125, False)
