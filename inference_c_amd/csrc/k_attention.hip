@@ -1159,8 +1159,14 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     // 11.2 -> 9.6, 8 heads x 1024^2 D 64 15.7 -> 13.8); over 2048 keys, or
     // with more blocks than CUs, the split plan stays faster (4 heads x
     // 2048^2 D 128 31.7 vs 35.7; 20 heads x 1024^2 D 64 17.0 vs 25.9).
+    // Exactly 256 such blocks (one per CU; not the 256-query plan) likewise
+    // take two key parts: 8 waves per CU instead of 4 (us, same box: 32 x
+    // 1024^2 D 64 non-causal 22.8 -> 18.7, 32q/8kv 1024 x 4096 D 128 109 ->
+    // 90, causal 32 x 1024 x 4096 D 64 (even key ranges) 77 -> 57; with 384
+    // blocks, two rounds, they lose: 48 x 1024^2 D 64 30.1 vs 34.1).
     const uint64_t q128 = ((sh.q_len + 127) / 128) * bhs;
-    const bool small_grid = !f32 && q128 >= 64 && q128 < 256;
+    const bool small_grid = !f32 && q128 >= 64 &&
+                            (q128 < 256 || (q128 == 256 && ((sh.q_len + 255) / 256) * bhs < 256));
     const bool small_short = small_grid && !causal && q128 <= 128 && sh.kv_len <= 1024;
     if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
         p.bm = 128;

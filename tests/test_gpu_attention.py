@@ -431,3 +431,24 @@ def test_short_small_grid_special_rows(sdk, orc):
     live = ~zero & ~np.isnan(want).any(axis=-1)
     assert live.any()
     check(got[live], want[live], weight[live], "f16", "ordinary rows")
+
+
+# f16, exactly 256 blocks of 128 queries (one per CU): two key parts per
+# query group, causal too when the key ranges are even (kv much longer than q).
+ROUND_SHAPES = [
+    ((1, 32, 8, 1024, 1024, 64, 64), False),
+    ((1, 32, 8, 1000, 1000, 128, 128), False),    # ragged query and key tiles
+    ((1, 64, 16, 512, 2048, 64, 64), True),       # causal offset 1536
+    ((2, 16, 16, 1024, 4096, 64, 64), True),      # causal offset 3072, batch 2
+]
+
+
+@pytest.mark.parametrize("shape,causal", ROUND_SHAPES)
+def test_one_round_key_parts(sdk, orc, shape, causal):
+    q, k, v, _ = inputs(orc, shape, "f16", 41, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, None, scale, causal, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, scale, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
+    check(got, want, weight, "f16", f"{shape} causal={causal}")
