@@ -1168,11 +1168,21 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const bool small_grid = !f32 && q128 >= 64 &&
                             (q128 < 256 || (q128 == 256 && ((sh.q_len + 255) / 256) * bhs < 256));
     const bool small_short = small_grid && !causal && q128 <= 128 && sh.kv_len <= 1024;
+    // f16 grids of fewer than 64 blocks of 128 queries: 64-query blocks of
+    // 4 waves (2 query groups x 2 key parts), the key range split over
+    // blocks as before (us, same box, one-part 64-query blocks -> two-part:
+    // 32q/8kv 128 x 2048 D 128 causal 33.3 -> 25.3, 8 x 512 x 4096 D 128
+    // causal 55.0 -> 39.7, 40q/8kv 64 x 4096 D 128 33.0 -> 25.3, 16 x 256 x
+    // 1024 D 64 15.5 -> 12.5, 8 x 512^2 D 128 14.7 -> 13.5).
+    const bool tiny_grid = !f32 && q128 < 64;
     if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
         p.bm = 128;
         p.key_parts = 2;
     } else if (small_grid) {
         p.bm = small_short ? 64 : 128;
+        p.key_parts = 2;
+    } else if (tiny_grid) {
+        p.bm = 64;
         p.key_parts = 2;
     } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
     else if (((sh.q_len + 127) / 128) * bhs >= 64) p.bm = 128;
@@ -1186,9 +1196,7 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0;
     auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
-    // (64-query blocks with two key parts are never split: the kernel has
-    // no split instance of them)
-    if (split && (p.key_parts == 1 || (small_grid && !small_short))) {
+    if (split && (p.key_parts == 1 || (small_grid && !small_short) || tiny_grid)) {
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
@@ -1312,10 +1320,12 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a);\
     } while (0)
-// f16 two-part blocks: also 64-query blocks (unsplit by construction)
+// f16 two-part blocks: also 64-query blocks
 #define ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, D, Q, K, V, M, O)                                     \
     do {                                                                                           \
-        if (plan.bm == 64)                                                                         \
+        if (plan.bm == 64 && split)                                                                \
+            hipLaunchKernelGGL((KERNEL<D, 64, false, true, 2>), grid, block, 0, s, Q, K, V, M, O, a); \
+        else if (plan.bm == 64)                                                                    \
             hipLaunchKernelGGL((KERNEL<D, 64, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a); \
         else                                                                                       \
             ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O);                                    \
