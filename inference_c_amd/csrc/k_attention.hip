@@ -1184,8 +1184,13 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     } else if (tiny_grid) {
         p.bm = 64;
         p.key_parts = 2;
-    } else if (!f32 && ((sh.q_len + 255) / 256) * bhs >= 256) p.bm = 256;
-    else if (((sh.q_len + 127) / 128) * bhs >= 64) p.bm = 128;
+    } else if (!f32) {
+        // more than 256 blocks of 128 queries: 256-query blocks, also below
+        // one round of them (us, same box, 128-query blocks -> 256: 48 x
+        // 1024^2 D 64 30.4 -> 29.7, 32q/8kv 1536^2 D 128 59.4 -> 58.0, causal
+        // 48q/8kv 1024 x 4096 D 128 135 -> 132)
+        p.bm = 256;
+    } else if (q128 >= 64) p.bm = 128;
     else p.bm = 64;
     p.tk = f32 ? 32 : 64;
     p.qblocks = (uint32_t)((sh.q_len + p.bm - 1) / p.bm);

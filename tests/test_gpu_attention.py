@@ -452,3 +452,17 @@ def test_one_round_key_parts(sdk, orc, shape, causal):
     want = orc.sdpa(q, k, v, None, scale, causal)
     weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
     check(got, want, weight, "f16", f"{shape} causal={causal}")
+
+
+# f16, more than 256 blocks of 128 queries but fewer than 256 of 256: the
+# 256-query plan below one round of blocks
+@pytest.mark.parametrize("shape,causal", [((1, 48, 12, 1000, 1000, 64, 64), False),
+                                          ((1, 64, 8, 520, 2100, 128, 128), True)])
+def test_partial_round_256_query_blocks(sdk, orc, shape, causal):
+    q, k, v, _ = inputs(orc, shape, "f16", 42, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, None, scale, causal, "f16")
+    q, k, v, got = head_subset(q, k, v, got)
+    want = orc.sdpa(q, k, v, None, scale, causal)
+    weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
+    check(got, want, weight, "f16", f"{shape} causal={causal}")
