@@ -1168,13 +1168,17 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const bool small_grid = !f32 && q128 >= 64 &&
                             (q128 < 256 || (q128 == 256 && ((sh.q_len + 255) / 256) * bhs < 256));
     const bool small_short = small_grid && !causal && q128 <= 128 && sh.kv_len <= 1024;
-    // f16 grids of fewer than 64 blocks of 128 queries: 64-query blocks of
-    // 4 waves (2 query groups x 2 key parts), the key range split over
-    // blocks as before (us, same box, one-part 64-query blocks -> two-part:
+    // Grids of fewer than 64 blocks of 128 queries: 64-query blocks of 4
+    // waves (2 query groups x 2 key parts), the key range split over blocks
+    // as before (us, same box, one-part 64-query blocks -> two-part: f16
     // 32q/8kv 128 x 2048 D 128 causal 33.3 -> 25.3, 8 x 512 x 4096 D 128
     // causal 55.0 -> 39.7, 40q/8kv 64 x 4096 D 128 33.0 -> 25.3, 16 x 256 x
-    // 1024 D 64 15.5 -> 12.5, 8 x 512^2 D 128 14.7 -> 13.5).
-    const bool tiny_grid = !f32 && q128 < 64;
+    // 1024 D 64 15.5 -> 12.5, 8 x 512^2 D 128 14.7 -> 13.5; f32 16 x 256 x
+    // 1024 D 64 34.7 -> 26.1, 4 x 1024^2 D 64 32.9 -> 24.6, 8 x 512^2 D 128
+    // 32.8 -> 25.1). f32 at D 128 over more keys keeps one part (its
+    // two-part 64-query block needs ~300 registers, one wave per SIMD:
+    // 32q/8kv 128 x 2048 63.6 vs 68.9, 8 x 512 x 4096 causal 103 vs 111).
+    const bool tiny_grid = q128 < 64 && (!f32 || sh.head_dim == 64 || sh.kv_len <= 512);
     if (f32 ? key_parts_pay_f32(sh, causal) : key_parts_pay(sh, causal)) {
         p.bm = 128;
         p.key_parts = 2;
@@ -1325,8 +1329,8 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             hipLaunchKernelGGL((KERNEL<D, 128, false, false, 2>), grid, block, 0, s, Q, K, V, M, O, a);\
     } while (0)
-// f16 two-part blocks: also 64-query blocks
-#define ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, D, Q, K, V, M, O)                                     \
+// two-part blocks of 64 or 128 queries
+#define ICSDK_FLASH_VARIANTS_KS2_BM(KERNEL, D, Q, K, V, M, O)                                     \
     do {                                                                                           \
         if (plan.bm == 64 && split)                                                                \
             hipLaunchKernelGGL((KERNEL<D, 64, false, true, 2>), grid, block, 0, s, Q, K, V, M, O, a); \
@@ -1335,16 +1339,16 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
         else                                                                                       \
             ICSDK_FLASH_VARIANTS_KS2(KERNEL, D, Q, K, V, M, O);                                    \
     } while (0)
-// the f32 kernel: 64- or 128-query blocks, 128-query blocks with two key
-// parts per query group
+// the f32 kernel: 64- or 128-query blocks, 64- or 128-query blocks with two
+// key parts per query group
 #define ICSDK_FLASH_SHAPES_F32(KERNEL, Q, K, V, M, O)                                              \
     do {                                                                                           \
         if (shape.head_dim == 64) {                                                                \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 64, Q, K, V, M, O);                      \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_BM(KERNEL, 64, Q, K, V, M, O);                   \
             else if (plan.bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 128, 1, Q, K, V, M, O);   \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 64, 1, Q, K, V, M, O);                        \
         } else {                                                                                   \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2(KERNEL, 128, Q, K, V, M, O);                     \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_BM(KERNEL, 128, Q, K, V, M, O);                  \
             else if (plan.bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 128, 1, Q, K, V, M, O);  \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
         }                                                                                          \
@@ -1355,12 +1359,12 @@ hipError_t combine_splits(const SdpaArgs &a, const FlashPlan &p, S *out, hipStre
     do {                                                                                           \
         const int bm = (int)plan.bm;                                                               \
         if (shape.head_dim == 64) {                                                                \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, 64, Q, K, V, M, O);                      \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_BM(KERNEL, 64, Q, K, V, M, O);                      \
             else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 256, 1, Q, K, V, M, O);        \
             else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 128, 1, Q, K, V, M, O);        \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 64, 64, 1, Q, K, V, M, O);                        \
         } else {                                                                                   \
-            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_F16(KERNEL, 128, Q, K, V, M, O);                     \
+            if (ks == 2) ICSDK_FLASH_VARIANTS_KS2_BM(KERNEL, 128, Q, K, V, M, O);                     \
             else if (bm == 256) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 256, 1, Q, K, V, M, O);       \
             else if (bm == 128) ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 128, 1, Q, K, V, M, O);       \
             else ICSDK_FLASH_VARIANTS_KS(KERNEL, 128, 64, 1, Q, K, V, M, O);                       \
@@ -1415,7 +1419,7 @@ hipError_t sdpa_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
 
 #undef ICSDK_FLASH_SHAPES_F16
 #undef ICSDK_FLASH_SHAPES_F32
-#undef ICSDK_FLASH_VARIANTS_KS2_F16
+#undef ICSDK_FLASH_VARIANTS_KS2_BM
 #undef ICSDK_FLASH_VARIANTS_KS2
 #undef ICSDK_FLASH_VARIANTS_KS
 
