@@ -1205,7 +1205,12 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
     const uint32_t ql = (uint32_t)sh.q_len, kl = (uint32_t)sh.kv_len;
     const uint32_t offset = kl > ql ? kl - ql : 0;
     auto tiles = [&](uint32_t j) { return flash_tiles(ql, kl, causal, offset, p.bm, p.tk, j); };
-    if (split && (p.key_parts == 1 || (small_grid && !small_short) || tiny_grid)) {
+    // f32 launches of two key parts in one round (256 blocks of 128
+    // queries) split the long blocks' key ranges as well (us, same box:
+    // causal 16 x 2048^2 D 64 171 -> 135, D 128 300 -> 228); from two rounds
+    // on the longest-first order balances them without the merge's traffic
+    const bool f32_round_split = f32 && p.key_parts == 2 && q128 <= 256;
+    if (split && (p.key_parts == 1 || (small_grid && !small_short) || tiny_grid || f32_round_split)) {
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;

@@ -277,6 +277,7 @@ KEY_PART_SHAPES = [
     (1, 128, 32, 500, 500, 64, 64),     # ragged query and key tiles
     (1, 64, 16, 700, 720, 64, 64),      # kv longer than q (causal offset 20), ragged
     (1, 64, 64, 512, 512, 128, 128),    # one q head per kv head
+    (1, 16, 4, 2048, 2048, 64, 64),     # one round of 256 blocks: long blocks' key ranges split too
 ]
 
 
