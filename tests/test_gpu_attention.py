@@ -467,3 +467,65 @@ def test_partial_round_256_query_blocks(sdk, orc, shape, causal):
     want = orc.sdpa(q, k, v, None, scale, causal)
     weight = orc.sdpa_abs_weight(q, k, v, None, scale, causal)
     check(got, want, weight, "f16", f"{shape} causal={causal}")
+
+
+def sdpa_f64(q, k, v, scale, causal):
+    """Float64 numpy restatement of the oracle's rule for finite inputs
+    without a mask (oracle/oracle.c sdpa_generic): query i sees key j unless
+    causal and j > i + max(kv_len - q_len, 0); softmax over the visible keys;
+    returns (out, sum_j p |v|)."""
+    b, h, lq, d = q.shape
+    kvh, lk = k.shape[1], k.shape[2]
+    group = h // kvh
+    kk = np.repeat(k.astype(np.float64), group, axis=1)
+    vv = np.repeat(v.astype(np.float64), group, axis=1)
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), kk) * scale
+    if causal:
+        offset = max(lk - lq, 0)
+        s = np.where(np.arange(lk)[None, :] > np.arange(lq)[:, None] + offset, -np.inf, s)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ vv, p @ np.abs(vv)
+
+
+def test_sdpa_f64_restatement_matches_oracle(orc):
+    """The float64 restatement used by the plan sweep against the oracle on
+    small causal (kv longer and shorter than q) and full shapes."""
+    for shape, causal in (((1, 4, 2, 37, 70, 64, 64), True), ((1, 2, 1, 70, 37, 64, 64), True),
+                          ((2, 2, 2, 33, 50, 128, 128), False)):
+        q, k, v, _ = inputs(orc, shape, "f32", 43, False)
+        scale = 1.0 / np.sqrt(shape[5])
+        want, weight = sdpa_f64(q, k, v, scale, causal)
+        got = orc.sdpa(q, k, v, None, scale, causal)
+        assert np.allclose(got, want, rtol=0, atol=1e-5 * weight.max())
+
+
+# Random shapes over every block plan (fewer than 64, 64-256 and more than
+# 256 blocks of 128 queries; ragged lengths, kv shorter and longer than q,
+# 1-8 q heads per kv head), drawn once with numpy's default_rng(2026).
+SWEEP_SHAPES = [
+    ((1, 1, 1, 548, 1547, 128, 128), True), ((2, 32, 8, 1082, 977, 128, 128), True),
+    ((2, 64, 16, 424, 1984, 64, 64), False), ((1, 64, 16, 690, 1244, 128, 128), True),
+    ((1, 4, 4, 406, 2057, 128, 128), True), ((1, 2, 2, 716, 1929, 128, 128), True),
+    ((1, 128, 16, 892, 892, 64, 64), True), ((1, 16, 4, 471, 527, 64, 64), True),
+    ((1, 8, 4, 870, 832, 128, 128), False), ((1, 16, 4, 558, 2303, 128, 128), True),
+    ((2, 4, 1, 866, 2479, 64, 64), False), ((2, 64, 16, 490, 1081, 64, 64), False),
+    ((1, 32, 4, 89, 2116, 64, 64), True), ((1, 8, 2, 625, 1711, 128, 128), False),
+    ((1, 64, 16, 241, 241, 128, 128), True), ((1, 16, 2, 154, 2040, 64, 64), True),
+    ((2, 32, 16, 259, 259, 128, 128), False), ((1, 16, 4, 989, 2466, 64, 64), True),
+    ((1, 8, 1, 102, 1794, 128, 128), False), ((1, 32, 16, 984, 1903, 128, 128), True),
+    ((1, 8, 4, 50, 2780, 128, 128), True), ((2, 64, 16, 989, 989, 128, 128), True),
+    ((1, 16, 2, 117, 404, 128, 128), False), ((1, 8, 4, 284, 2881, 64, 64), False),
+]
+
+
+@pytest.mark.parametrize("shape,causal", SWEEP_SHAPES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_plan_sweep(sdk, orc, shape, causal, dtype):
+    q, k, v, _ = inputs(orc, shape, dtype, 44, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, None, scale, causal, dtype)
+    q, k, v, got = head_subset(q, k, v, got)
+    want, weight = sdpa_f64(q, k, v, scale, causal)
+    want = want.astype(np.float16 if dtype == "f16" else np.float32)   # the output's rounding
+    check(got, want, weight, dtype, f"{shape} causal={causal}")
