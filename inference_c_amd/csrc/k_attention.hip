@@ -1074,7 +1074,8 @@ namespace {
 // launch are split: target split_tiles = max(total key tiles / slots,
 // kMinPartTiles), slots measured over 128 .. 3072: f16 128 (a split rarely
 // pays for its merge: the vision shape is best in 2 parts, 32 x 2048^2
-// causal unsplit; tiny grids still split), f32 512 (its 32-key tiles of
+// causal unsplit; grids of up to 256 blocks of 128 queries take 256 and
+// the parts fitted to one round, below), f32 512 (its 32-key tiles of
 // 64 MFMAs keep a block busy: 12 x 1024^2 D 64 53 us in 6 parts vs 59 in
 // 2 and 103 unsplit; 4 x 16 x 512^2, 256 blocks, is best unsplit). Items
 // beyond kMaxFlashItems per (batch, head): descending query blocks, no
@@ -1214,9 +1215,34 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         uint64_t total = 0;
         for (uint32_t j = 0; j < p.qblocks; ++j) total += tiles(j);
         total *= bhs;
-        const uint64_t slots = f32 ? 512 : 128;
+        // f16 grids of up to 256 blocks (one per CU: the two-part blocks
+        // take up to 151 KB of LDS) cut their key ranges into the most
+        // parts that still fit one round of 256 blocks (us, same box, 128
+        // slots before: 32q/8kv decode over 16384 keys 64.5 -> 37.0, 4 x
+        // 32q/8kv decode over 2048 keys 34.2 -> 22.5, 32q/8kv 16 x 4096 causal
+        // 22.8 -> 16.6, 8 x 512 x 4096 causal 39.5 -> 28.3, 8 x 1024 x 8192
+        // 76.7 -> 54.3, 16 x 1024 x 4096 causal 48.7 -> 37.0; others equal)
+        const bool fit = !f32 && (tiny_grid || small_grid);
+        const uint64_t slots = f32 ? 512 : fit ? 256 : 128;
         const uint64_t target = (total + slots - 1) / slots;
         p.split_tiles = (uint32_t)(target > kMinPartTiles ? target : kMinPartTiles);
+        if (fit) {
+            // the smallest part size whose parts fit 256 blocks (the part
+            // count never grows with the part size: a binary search)
+            auto parts_total = [&](uint32_t st) {
+                uint64_t n = 0;
+                for (uint32_t j = 0; j < p.qblocks; ++j) n += split_parts(tiles(j), st);
+                return n * bhs;
+            };
+            uint32_t lo = p.split_tiles, hi = lo;
+            for (uint32_t j = 0; j < p.qblocks; ++j) hi = tiles(j) > hi ? tiles(j) : hi;
+            while (lo < hi) {
+                const uint32_t mid = lo + (hi - lo) / 2;
+                if (parts_total(mid) <= 256) hi = mid;
+                else lo = mid + 1;
+            }
+            p.split_tiles = lo;
+        }
     }
     struct Item {
         uint32_t size, qblock, part, parts;
