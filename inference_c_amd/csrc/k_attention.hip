@@ -1226,23 +1226,27 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         const uint64_t slots = f32 ? 512 : fit ? 256 : 128;
         const uint64_t target = (total + slots - 1) / slots;
         p.split_tiles = (uint32_t)(target > kMinPartTiles ? target : kMinPartTiles);
-        if (fit) {
-            // the smallest part size whose parts fit 256 blocks (the part
-            // count never grows with the part size: a binary search)
-            auto parts_total = [&](uint32_t st) {
-                uint64_t n = 0;
-                for (uint32_t j = 0; j < p.qblocks; ++j) n += split_parts(tiles(j), st);
-                return n * bhs;
-            };
-            uint32_t lo = p.split_tiles, hi = lo;
-            for (uint32_t j = 0; j < p.qblocks; ++j) hi = tiles(j) > hi ? tiles(j) : hi;
-            while (lo < hi) {
-                const uint32_t mid = lo + (hi - lo) / 2;
-                if (parts_total(mid) <= 256) hi = mid;
-                else lo = mid + 1;
-            }
-            p.split_tiles = lo;
+        // The smallest part size from there whose items fit the work table
+        // (kMaxFlashItems per (batch, head)) and, for `fit`, 256 blocks in
+        // all. The item count never grows with the part size, so a binary
+        // search; at the largest size every query block is one item.
+        auto parts_of = [&](uint32_t st) {
+            uint64_t n = 0;
+            for (uint32_t j = 0; j < p.qblocks; ++j) n += split_parts(tiles(j), st);
+            return n;
+        };
+        auto fits = [&](uint32_t st) {
+            const uint64_t n = parts_of(st);
+            return n <= kMaxFlashItems && (!fit || n * bhs <= 256);
+        };
+        uint32_t lo = p.split_tiles, hi = lo;
+        for (uint32_t j = 0; j < p.qblocks; ++j) hi = tiles(j) > hi ? tiles(j) : hi;
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            if (fits(mid)) hi = mid;
+            else lo = mid + 1;
         }
+        p.split_tiles = lo;
     }
     struct Item {
         uint32_t size, qblock, part, parts;
@@ -1254,6 +1258,8 @@ FlashPlan flash_plan(const k::SdpaShape &sh, bool aligned, bool f32, bool causal
         const uint32_t share = (t + parts - 1) / parts;
         if (n + parts > kMaxFlashItems) {   // too many: descending query blocks, whole
             p.split_tiles = 0;
+            p.max_parts = 1;
+            p.first_split = p.qblocks;
             return p;
         }
         for (uint32_t q = 0; q < parts; ++q) {

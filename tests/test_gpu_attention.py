@@ -529,3 +529,22 @@ def test_plan_sweep(sdk, orc, shape, causal, dtype):
     want, weight = sdpa_f64(q, k, v, scale, causal)
     want = want.astype(np.float16 if dtype == "f16" else np.float32)   # the output's rounding
     check(got, want, weight, dtype, f"{shape} causal={causal}")
+
+
+# Long query ranges with few heads: split key ranges whose items would
+# overflow the work table (128 per batch and head) take larger parts until
+# they fit (before, such plans fell back to whole query blocks but kept a
+# stale part count, so the split kernel ran without a split).
+@pytest.mark.parametrize("shape,causal", [
+    ((1, 2, 2, 2041, 2301, 64, 64), False), ((1, 2, 1, 1425, 3753, 64, 64), False),
+    ((1, 4, 2, 1657, 2158, 128, 128), True), ((1, 1, 1, 2500, 3000, 128, 128), False),
+    ((1, 1, 1, 3000, 4000, 64, 64), True)])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_split_work_table_limit(sdk, orc, shape, causal, dtype):
+    q, k, v, _ = inputs(orc, shape, dtype, 45, False)
+    scale = 1.0 / np.sqrt(shape[5])
+    got = run_device(sdk, q, k, v, None, scale, causal, dtype)
+    q, k, v, got = head_subset(q, k, v, got)
+    want, weight = sdpa_f64(q, k, v, scale, causal)
+    want = want.astype(np.float16 if dtype == "f16" else np.float32)
+    check(got, want, weight, dtype, f"{shape} causal={causal}")
