@@ -1077,9 +1077,9 @@ namespace {
 // causal unsplit; grids of up to 256 blocks of 128 queries take 256 and
 // the parts fitted to one round, below), f32 512 (its 32-key tiles of
 // 64 MFMAs keep a block busy: 12 x 1024^2 D 64 53 us in 6 parts vs 59 in
-// 2 and 103 unsplit; 4 x 16 x 512^2, 256 blocks, is best unsplit). Items
-// beyond kMaxFlashItems per (batch, head): descending query blocks, no
-// split.
+// 2 and 103 unsplit; 4 x 16 x 512^2, 256 blocks, is best unsplit). The
+// part size grows until a (batch, head)'s items fit kMaxFlashItems; more
+// query blocks than that: descending query blocks, no split.
 struct FlashPlan {
     bool flash = false;
     uint32_t bm = 64, tk = 64;   // queries per block (64, 128, or 256 for f16), keys per tile
