@@ -548,3 +548,56 @@ def test_split_work_table_limit(sdk, orc, shape, causal, dtype):
     want, weight = sdpa_f64(q, k, v, scale, causal)
     want = want.astype(np.float16 if dtype == "f16" else np.float32)
     check(got, want, weight, dtype, f"{shape} causal={causal}")
+
+
+def sdpa_f64_masked(q, k, v, mask, scale, causal):
+    """sdpa_f64 with an optional additive [Lq, Lkv] mask (entries may be
+    -inf; every row here keeps a finite score)."""
+    b, h, lq, d = q.shape
+    kvh, lk = k.shape[1], k.shape[2]
+    group = h // kvh
+    kk = np.repeat(k.astype(np.float64), group, axis=1)
+    vv = np.repeat(v.astype(np.float64), group, axis=1)
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), kk) * scale
+    if mask is not None:
+        s = s + mask.astype(np.float64)
+    if causal:
+        offset = max(lk - lq, 0)
+        s = np.where(np.arange(lk)[None, :] > np.arange(lq)[:, None] + offset, -np.inf, s)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ vv, p @ np.abs(vv)
+
+
+def test_sdpa_f64_masked_matches_oracle(orc):
+    for shape, causal in (((1, 2, 1, 37, 70, 32, 16), True), ((1, 2, 2, 40, 33, 64, 64), False)):
+        q, k, v, mask = inputs(orc, shape, "f32", 46, True)
+        want, weight = sdpa_f64_masked(q, k, v, mask, -0.1, causal)
+        got = orc.sdpa(q, k, v, mask, -0.1, causal)
+        assert np.allclose(got, want, rtol=0, atol=1e-5 * weight.max())
+
+
+# Mixed cases drawn once with default_rng(11): masks, scales of zero and
+# below (the general variant), head dims off the MFMA path (the row
+# kernel), D != Dv, short and long key ranges.
+MIXED_CASES = [
+    ((1, 4, 1, 1567, 87, 32, 32), True, False, -0.1), ((1, 8, 8, 1733, 743, 64, 64), False, False, -0.1),
+    ((1, 1, 1, 1218, 2471, 128, 64), True, False, 0.05), ((1, 2, 2, 1886, 2020, 64, 32), True, False, 0.0),
+    ((1, 4, 2, 9, 2989, 128, 128), True, False, 0.0), ((1, 8, 1, 1293, 61, 16, 16), True, True, 0.05),
+    ((2, 1, 1, 18, 1399, 128, 128), True, False, 0.0), ((2, 4, 1, 1970, 2220, 32, 32), False, True, 0.176777),
+    ((1, 2, 1, 2067, 2181, 128, 128), True, False, 0.0), ((1, 16, 2, 237, 203, 128, 128), True, True, 0.088388),
+    ((1, 16, 4, 316, 1990, 128, 128), False, False, 0.05), ((1, 8, 8, 1407, 490, 32, 32), False, True, 0.0),
+    ((1, 2, 1, 15, 116, 96, 96), True, False, 0.05), ((1, 8, 2, 775, 276, 128, 128), True, False, 0.088388),
+    ((1, 1, 1, 652, 1494, 64, 64), True, False, -0.1), ((1, 16, 4, 1481, 2295, 128, 128), True, False, -0.1),
+]
+
+
+@pytest.mark.parametrize("shape,causal,masked,scale", MIXED_CASES)
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_mixed_cases(sdk, orc, shape, causal, masked, scale, dtype):
+    q, k, v, mask = inputs(orc, shape, dtype, 47, masked)
+    got = run_device(sdk, q, k, v, mask, scale, causal, dtype)
+    q, k, v, got = head_subset(q, k, v, got)
+    want, weight = sdpa_f64_masked(q, k, v, mask, scale, causal)
+    want = want.astype(np.float16 if dtype == "f16" else np.float32)
+    check(got, want, weight, dtype, f"{shape} causal={causal} mask={masked} scale={scale}")
