@@ -308,6 +308,9 @@ QUANT_SHAPES = [  # rows, in, out
     # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
+    # drawn once with numpy's default_rng(5): rows 1-40, in up to 16384
+    (16, 13216, 68), (17, 7712, 1546), (8, 4704, 2938), (1, 4576, 1150), (8, 6720, 394),
+    (1, 16384, 573), (3, 7136, 790), (40, 2912, 2693), (4, 10304, 1479), (1, 15744, 1667),
 ]
 
 
