@@ -194,3 +194,28 @@ def test_view_rejects_out_of_bounds(sdk):
     bad = sdk.tensor("f16", (3, 10))
     ok, msg = sdk.try_call("tensor_view_add_mul_f16", x, TensorView.make((10, 10), (10, 1), 0), bad, None, y)
     assert not ok and "1 or equal" in msg
+
+
+# Views drawn once at random (numpy default_rng(13)): permutations of a
+# contiguous base, slices, a stride-0 dim, operands broadcast over random
+# dims; bit-exact against the oracle.
+RANDOM_VIEWS = [  # dtype, base shape, view shape, strides, offset, addend shape, multiplier shape
+    ("f32", (3, 2, 1, 100, 257), (1, 2, 100, 3, 257), (25700, 25700, 257, 51400, 1), 0, (1, 2, 1, 3, 1), None),
+    ("f32", (128, 32, 16, 7, 3), (7, 128, 3, 32, 16), (3, 10752, 1, 336, 21), 0, None, (1, 128, 3, 1, 1)),
+    ("f32", (32, 3, 32, 1, 1), (1, 1, 3, 32, 32), (1, 1, 32, 1, 96), 0, (1, 1, 1, 1, 1), (1, 1, 1, 32, 32)),
+    ("f16", (100,), (44,), (1,), 56, (1,), None),
+    ("f16", (257, 3, 257, 3), (257, 2, 3, 257), (2313, 1, 771, 3), 1, (257, 2, 3, 257), (1, 2, 1, 257)),
+    ("f32", (7, 7), (7, 7), (1, 7), 0, (7, 1), (1, 7)),
+    ("f16", (64, 16, 128), (16, 128, 64), (128, 1, 2048), 0, (16, 1, 64), None),
+    ("f16", (100, 32, 7), (7, 100, 32), (1, 224, 7), 0, (1, 1, 1), (7, 100, 32)),
+    ("f16", (16, 64, 3), (3, 64, 16), (1, 3, 192), 0, None, None),
+]
+
+
+@pytest.mark.parametrize("case", RANDOM_VIEWS)
+def test_random_views(sdk, orc, case):
+    dt, base, shape, strides, off, ashape, mshape = case
+    x = orc.normal(base, 70, 0, 0.0, 1.0, dt)
+    A = None if ashape is None else orc.uniform(ashape, 70, 1, -1.0, 1.0, dt)
+    M = None if mshape is None else orc.uniform(mshape, 70, 2, -1.0, 1.0, dt)
+    view_case(sdk, orc, x, shape, strides, off, A, M, dtype=dt)
