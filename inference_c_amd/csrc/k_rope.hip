@@ -233,7 +233,167 @@ __global__ __launch_bounds__(kBlock) void rope_fused_kernel(S *__restrict__ q, S
     }
 }
 
+// ---- group path ------------------------------------------------------------
+
+// Shapes whose q rows and k rows each fill whole groups of 32 (row, chunk)
+// items (qh * kChunks and kh * kChunks multiples of 32). A group is then a
+// contiguous 1 KB run of one tensor at one position (32 / kChunks rows of
+// 2 * half elements), and group n of a tensor is simply its bytes
+// n * 1024 .. n * 1024 + 1023. Lane l < 32 of a wave holds the left vector
+// of row (l % 32) / kChunks, chunk l % kChunks of a group, lane l + 32 the
+// right vector of the same pairs, so a lane's offset inside a group is a
+// constant of its lane number.
+//
+// Blocks alternate between the tensors (even blocks q, odd blocks k, while
+// both have blocks left; then the larger one's), so at any time the grid
+// streams q and k of neighbouring positions. Wave w of a tensor's blocks
+// owns that tensor's groups w * kIt .. w * kIt + kIt - 1: its offsets are
+// linear in the group number and need no per-group scalar work; a group
+// past the tensor's end gets an offset beyond the tensor's buffer range (its
+// loads return zeros, the hardware drops its stores). Each wave computes the
+// rotations of the positions its groups touch into its own slice of LDS (no
+// block barrier, no serial set-up); each lane turns its chunk's (cos, sin)
+// into the coefficients of its side -- left lanes l' = l*c + r*(-s), right
+// lanes r' = l*s + r*c, the same two products and one sum as l*c - r*s and
+// r*c + l*s -- and per group it does one 16-byte load, four
+// v_permlane32_swap and E pairs of products.
+//
+// Why this layout (measured on MI355X at configs[4]'s shape, q and k
+// [4096, 32, 64] f16, back to back over rotated sets): all waves of the
+// launch start together, and scalar instructions in front of a wave's first
+// load delay it while the CU's one scalar unit serves 16 waves. The fused
+// kernel below (generic item math) ran 145 scalar and 907 vector
+// instructions per wave, 13.1 us; the same work numbered position-major
+// (a position's q groups then its k groups) needed ~130 scalar instructions
+// before the first load, 12.5 us; this layout 25, 11.9 us, against 11.5 us
+// for an in-place copy of the same bytes.
+constexpr uint32_t kGroupBytes = 1024;        // 32 items x 2 vectors x 16 bytes
+constexpr uint32_t kDeadOffset = 0xfffff000u;  // beyond any buffer range the host allows
+
+// Arguments: everything a wave needs before its first load comes first, as
+// plain scalars, so that it arrives preloaded in SGPRs (an aggregate argument
+// ends the preloaded run); q_mul/q_shift and k_mul/k_shift are the
+// multiply-high divisions by qg and kg (FastDiv).
+template <typename S, int kChunks, int kIt>
+__global__ __launch_bounds__(kBlock) void rope_group_kernel(
+    S *__restrict__ q, S *__restrict__ k, uint32_t q_bytes, uint32_t k_bytes, uint32_t nbq,
+    uint32_t nbk, uint32_t qg, uint32_t q_mul, uint32_t q_shift, uint32_t kg, uint32_t k_mul,
+    uint32_t k_shift, uint32_t npos_w, uint64_t offset, RopeDenoms denom) {
+    constexpr uint32_t E = Vec16<S>::N;
+    constexpr uint32_t half = kChunks * E;
+    extern __shared__ float2 rot[];   // per wave: npos_w * half rotations
+    const uint32_t lane = threadIdx.x & (kWave - 1), side = lane >> 5, c = lane % kChunks;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    float2 *const mine = rot + wave * npos_w * half;
+    const uint32_t lane_off =
+        (((lane & 31) / kChunks) * 2 * half + c * E + side * half) * (uint32_t)sizeof(S);
+    // this block's tensor and its block index in that tensor
+    const uint32_t both = min(nbq, nbk);
+    const bool in_q = blockIdx.x < 2 * both ? (blockIdx.x & 1u) == 0 : nbq > nbk;
+    const uint32_t bt = blockIdx.x < 2 * both ? blockIdx.x >> 1 : blockIdx.x - both;
+    const uint32_t g0 = (bt * (kBlock / kWave) + wave) * kIt;
+    // groups per position of this tensor
+    const FastDiv div = in_q ? FastDiv{qg, q_mul, q_shift} : FastDiv{kg, k_mul, k_shift};
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        in_q ? q : k, 0, (int)(in_q ? q_bytes : k_bytes), kRawBufferWord3);
+    // groups of this wave inside the tensor; the others get an offset
+    // beyond every buffer range (<= 2^31 bytes), so the hardware returns
+    // zeros for their loads and drops their stores
+    const uint32_t bytes = in_q ? q_bytes : k_bytes;
+    const uint32_t live = bytes / kGroupBytes > g0 ? bytes / kGroupBytes - g0 : 0u;
+    uint32_t off[kIt];
+#pragma unroll
+    for (int u = 0; u < kIt; ++u) off[u] = (g0 + u) * kGroupBytes + lane_off;
+    if (live < (uint32_t)kIt) {   // wave-uniform: only a tensor's last waves
+#pragma unroll
+        for (int u = 0; u < kIt; ++u)
+            if ((uint32_t)u >= live) off[u] = kDeadOffset;
+    }
+    Vec16<S> v[kIt];
+#pragma unroll
+    for (int u = 0; u < kIt; ++u)
+        v[u] = __builtin_bit_cast(Vec16<S>, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs, (int)off[u], 0, kPolicyStream));
+    // the groups' positions, relative to the wave's first (scalar)
+    const uint32_t p_first = fast_div(g0, div);
+    uint32_t rel[kIt];
+    {
+        uint32_t j = g0 - p_first * div.divisor, r = 0;
+#pragma unroll
+        for (int u = 0; u < kIt; ++u) {
+            rel[u] = r;
+            const bool wrap = ++j == div.divisor;
+            j = wrap ? 0u : j;
+            r += wrap ? 1u : 0u;
+        }
+    }
+    const uint32_t entries = (rel[kIt - 1] + 1) * half;
+    for (uint32_t e = lane; e < entries; e += kWave) {
+        const uint32_t d = e % half;
+        const float angle = (float)((double)(offset + p_first + e / half) / denom.d[d]);
+        float cs, sn;
+        sincosf(angle, &sn, &cs);
+        mine[e] = make_float2(cs, sn);
+    }
+    // the slice is this wave's alone: its writes before the other lanes' reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float ca[E], cb[E];   // this side's coefficients of the left and right values
+#pragma unroll
+    for (int u = 0; u < kIt; ++u) {
+        if (u == 0 || rel[u] != rel[u - 1]) {   // wave-uniform
+            const float2 *t = mine + rel[u] * half + c * E;
+#pragma unroll
+            for (uint32_t e = 0; e < E; ++e) {
+                const float2 cs = t[e];
+                ca[e] = side ? cs.y : cs.x;
+                cb[e] = side ? cs.x : -cs.y;
+            }
+        }
+        const uint4 words = __builtin_bit_cast(uint4, v[u]);
+        const uint32_t w[4] = {words.x, words.y, words.z, words.w};
+        uint32_t lw[4], rw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // lanes 0-31 keep their word in the first result and receive lane
+            // + 32's in the second; lanes 32-63 the reverse: in every lane the
+            // first result is the left vector, the second the right one
+            const auto r = __builtin_amdgcn_permlane32_swap(w[i], w[i], false, false);
+            lw[i] = r[0];
+            rw[i] = r[1];
+        }
+        const Vec16<S> lv = __builtin_bit_cast(Vec16<S>, uint4{lw[0], lw[1], lw[2], lw[3]});
+        const Vec16<S> rv = __builtin_bit_cast(Vec16<S>, uint4{rw[0], rw[1], rw[2], rw[3]});
+        Vec16<S> out;
+#pragma unroll
+        for (uint32_t e = 0; e < E; ++e)
+            out.v[e] = Elem<S>::store(Elem<S>::load(lv.v[e]) * ca[e] +
+                                      Elem<S>::load(rv.v[e]) * cb[e]);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), rs, (int)off[u], 0,
+                                               kPolicyDeviceScope);
+    }
+}
+
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Vectors per half row on the group path, or 0 when the shape does not fit it.
+template <typename S>
+uint32_t group_chunks(size_t seq, size_t qh, size_t kh, size_t dim, const void *q,
+                      const void *k) {
+    constexpr size_t E = Vec16<S>::N;
+    const size_t half = dim / 2;
+    if (half % E != 0 || half > (size_t)kMaxHalf || !aligned16(q) || !aligned16(k)) return 0;
+    const size_t chunks = half / E;
+    if (chunks != 1 && chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16 && chunks != 32)
+        return 0;
+    if ((qh * chunks) % 32 != 0 || (kh * chunks) % 32 != 0) return 0;
+    // byte offsets in 32 bits, with kDeadOffset beyond every tensor
+    const size_t q_bytes = seq * qh * dim * sizeof(S), k_bytes = seq * kh * dim * sizeof(S);
+    if (q_bytes > (size_t{1} << 31) || k_bytes > (size_t{1} << 31) || seq > (size_t{1} << 24))
+        return 0;
+    return (uint32_t)chunks;
+}
 
 // Vectors per half row on the fused path, or 0 when the shape takes the
 // table path.
@@ -259,6 +419,50 @@ hipError_t launch_rope(S *q, S *k, size_t seq, size_t qh, size_t kh, size_t dim,
     if (dim == 0 || dim % 2 || seq * half > 0xffffffffu || qh + kh > 0xffffffu)
         return hipErrorInvalidValue;
     const size_t heads = qh + kh;
+    if (const uint32_t chunks = group_chunks<S>(seq, qh, kh, dim, q, k)) {
+        RopeDenoms denom{};
+        for (size_t d = 0; d < half; ++d)
+            denom.d[d] = std::pow(theta, (2.0 * (double)d) / (double)dim);
+        // groups per position of each tensor, and in all
+        const uint32_t qg = (uint32_t)(qh * chunks / 32), kg = (uint32_t)(kh * chunks / 32);
+        const size_t groups = seq * (size_t)(qg + kg);
+        // groups per wave: 8 loads in flight per lane while that leaves at
+        // least 1024 blocks (configs[4]: 32768 groups, 1024 blocks of 4 waves)
+        const int it = groups >= 32768 ? 8 : groups >= 16384 ? 4 : groups >= 8192 ? 2 : 1;
+        const size_t per_block = (size_t)it * (kBlock / kWave);
+        const uint32_t nbq = (uint32_t)((seq * qg + per_block - 1) / per_block);
+        const uint32_t nbk = (uint32_t)((seq * kg + per_block - 1) / per_block);
+        const dim3 grid(nbq + nbk), block(kBlock);
+        // positions one wave's groups can touch (its first group anywhere in a position)
+        const uint32_t gmin = qg < kg ? qg : kg;
+        const uint32_t npos_w = (uint32_t)((it + gmin - 2) / gmin + 1);
+        const size_t lds = (size_t)(kBlock / kWave) * npos_w * half * sizeof(float2);
+        const uint32_t qb = (uint32_t)(seq * qh * dim * sizeof(S)),
+                       kb = (uint32_t)(seq * kh * dim * sizeof(S));
+        const FastDiv q_div = make_fast_div(qg), k_div = make_fast_div(kg);
+#define ICSDK_ROPE_G(CH, IT)                                                                    \
+    hipLaunchKernelGGL((rope_group_kernel<S, CH, IT>), grid, block, lds, s, q, k, qb, kb, nbq,  \
+                       nbk, qg, q_div.multiplier, q_div.shift, kg, k_div.multiplier,            \
+                       k_div.shift, npos_w, (uint64_t)offset, denom)
+#define ICSDK_ROPE_G_IT(CH)                                                                     \
+    do {                                                                                        \
+        if (it == 1) ICSDK_ROPE_G(CH, 1);                                                       \
+        else if (it == 2) ICSDK_ROPE_G(CH, 2);                                                  \
+        else if (it == 4) ICSDK_ROPE_G(CH, 4);                                                  \
+        else ICSDK_ROPE_G(CH, 8);                                                               \
+    } while (0)
+        switch (chunks) {
+            case 1: ICSDK_ROPE_G_IT(1); break;
+            case 2: ICSDK_ROPE_G_IT(2); break;
+            case 4: ICSDK_ROPE_G_IT(4); break;
+            case 8: ICSDK_ROPE_G_IT(8); break;
+            case 16: ICSDK_ROPE_G_IT(16); break;
+            default: ICSDK_ROPE_G_IT(32); break;
+        }
+#undef ICSDK_ROPE_G_IT
+#undef ICSDK_ROPE_G
+        return hipGetLastError();
+    }
     if (const uint32_t chunks = fused_chunks<S>(seq, qh, kh, dim, q, k)) {
         RopeDenoms denom{};
         for (size_t d = 0; d < half; ++d)
@@ -326,8 +530,10 @@ namespace k {
 
 size_t rope_table_bytes(size_t seq, size_t qh, size_t kh, size_t dim, size_t elem,
                         const void *q, const void *k) {
-    const bool fused = elem == 4 ? fused_chunks<float>(seq, qh, kh, dim, q, k) != 0
-                                 : fused_chunks<_Float16>(seq, qh, kh, dim, q, k) != 0;
+    const bool fused = elem == 4 ? group_chunks<float>(seq, qh, kh, dim, q, k) != 0 ||
+                                       fused_chunks<float>(seq, qh, kh, dim, q, k) != 0
+                                 : group_chunks<_Float16>(seq, qh, kh, dim, q, k) != 0 ||
+                                       fused_chunks<_Float16>(seq, qh, kh, dim, q, k) != 0;
     return fused ? 0 : seq * (dim / 2) * sizeof(float2);
 }
 

@@ -72,6 +72,9 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // Cache policy of a store with device scope (SC1): the line is written
 // through this XCD's L2 towards memory instead of being left dirty in it.
 constexpr int kPolicyDeviceScope = 16;
+// Cache policy of a streaming load (NT), as __builtin_nontemporal_load gives
+// a global load: the line is not kept for reuse.
+constexpr int kPolicyStream = 2;
 
 // A window of at most 4 GiB of output, addressed by 32-bit byte offsets from
 // a base that is the same for every lane of the wave (a kernel argument plus
