@@ -54,7 +54,10 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const T *__restrict__ x, c
                                                       uint32_t rows, uint32_t in, uint32_t out) {
     constexpr uint32_t E = 16 / sizeof(T);
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * kBlock + threadIdx.x) / kWave);
+    // the wave's index in the grid, formed without the work-item number
+    // (blockIdx.x * kBlock), which would wrap in 32 bits for a large grid
+    const uint32_t wave =
+        __builtin_amdgcn_readfirstlane(blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave);
     const uint32_t o0 = wave * O;
     if (o0 >= out) return;
     const uint32_t r0 = blockIdx.y * R;
@@ -143,9 +146,13 @@ hipError_t gemv(const T *x, const T *w, const T *bias, T *y, size_t rows, size_t
 hipError_t linear_gemv(bool f32, const void *x, const void *w, const void *bias, void *y,
                        size_t rows, size_t in, size_t out, hipStream_t s) {
     const size_t elem = f32 ? 4 : 2;
-    // out < 2^32 keeps grid.x (out / O waves, 4 per block) within its limit
+    // The launch is one wave (64 work-items) per output row: out * 64 must
+    // stay below 2^32, the dispatch packet's work-item count. Larger `out`
+    // is declined here (hipErrorNotSupported), and the caller takes the
+    // library GEMM.
     if (rows == 0 || rows > kGemvMaxRows || in == 0 || out == 0 || in % (16 / elem) != 0 ||
-        in > 0xffffffffu || out > 0xffffffffu || (((uintptr_t)x | (uintptr_t)w) & 15u) != 0)
+        in > 0xffffffffu || out > 0xffffffffu / kWave ||
+        (((uintptr_t)x | (uintptr_t)w) & 15u) != 0)
         return hipErrorNotSupported;
     if (f32)
         return gemv(static_cast<const float *>(x), static_cast<const float *>(w),

@@ -149,6 +149,31 @@ __device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const Gemv
     }
 }
 
+// 2^-24 * sum_k x_k w_k of one block, decoded value by value with the signed
+// weights (the reference's own decode, tensor_compute_cuda.cu:229-234). The
+// path for a block whose x holds an infinity or NaN: the offset decode forms
+// x (w + offset) - offset x, which turns x = +-Inf into Inf - Inf = NaN where
+// the reference's x * (scale w) gives +-Inf (NaN only for w = 0 or mixed
+// signs). `values` are the block's value bytes, `x` its 32 f16 (global
+// memory or LDS). A rolled loop over memory operands: it runs only for
+// non-finite input and adds no registers to the kernels' common path.
+template <bool kQ8>
+__device__ inline float exact_block(const uint8_t *values, const _Float16 *x) {
+    float s = 0.0f;
+#pragma unroll 1
+    for (int k = 0; k < 32; ++k) {
+        int q;
+        if constexpr (kQ8) {
+            q = (int)(int8_t)values[k];
+        } else {
+            const uint8_t packed = values[k & 15];
+            q = (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
+        }
+        s = __builtin_fmaf((float)x[k], (float)q * 0x1p-24f, s);
+    }
+    return s;
+}
+
 // Grid: x = waves of O output rows (4 waves per block), y = groups of R
 // input rows. Requires x rows 16-byte aligned, w 4-byte aligned, in % 32 == 0.
 template <bool kQ8, int R, int O, bool kSplit>
@@ -228,6 +253,7 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         const uint32_t b = c0 + min(lane, nb - 1);
         uint32_t xv[R][16];
         float base[R];   // -offset * 2^-24 * (the x sum of the lane's block)
+        bool nonfinite[R];   // the block's x holds an infinity or NaN
         const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -246,9 +272,16 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
                 xs0 = __builtin_amdgcn_fdot2(as_half2(xv[r][i]), one2, xs0, false);
                 xs1 = __builtin_amdgcn_fdot2(as_half2(xv[r][i + 1]), one2, xs1, false);
             }
-            // -offset * 2^-24 * sum (exact: a power of two times the sum)
+            // -offset * 2^-24 * sum (exact: a power of two times the sum).
+            // 32 finite f16 sum to at most 2^21 in magnitude, so the sum is
+            // non-finite exactly when one of them is.
             base[r] = (xs0 + xs1) * (kQ8 ? -0x1p-17f : -0x1p-21f);
+            nonfinite[r] = !__builtin_isfinite(xs0 + xs1);
         }
+        bool any = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) any |= nonfinite[r];
+        const bool redo = __builtin_amdgcn_ballot_w64(any) != 0;   // wave-uniform
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
@@ -270,6 +303,19 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
             float dot[R];
             gemv_block<kQ8, R>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0, xv, base, scale,
                                dot);
+            if (redo) {
+                // rare: a non-finite x in some lane's block. Those blocks are
+                // recomputed with the signed decode; a lane past the chunk's
+                // end (whose x is the last block's, possibly non-finite) adds 0
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (!live) dot[r] = 0.0f;
+                    else if (nonfinite[r])
+                        dot[r] = exact_block<kQ8>(region[o] + off + 2,
+                                                  reinterpret_cast<const _Float16 *>(xrow[r]) +
+                                                      (uint64_t)b * 32);
+                }
+            }
             // a lane past the chunk's end adds 0 * (a finite dot)
             const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(live ? scale : 0u));
 #pragma unroll
@@ -533,12 +579,44 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(scale, d[i], acc[i]);
         };
+        const f32x4 acc_in = acc;
         if (nb == kChunk) {
             static_for<kChunk>([&](auto jc) { block(jc); });
         } else {
             static_for<kChunk>([&](auto jc) {
                 if ((uint32_t)decltype(jc)::value < nb) block(jc);
             });
+        }
+        // A row whose x holds an infinity or NaN in this chunk: the offset
+        // MFMA turns x * w into x * (w + offset) - offset * x, NaN for
+        // x = +-Inf where the reference gives +-Inf. Finite x keeps every
+        // partial finite, so a live row whose sum turned non-finite here is
+        // redone from the chunk's start with the signed decode (rare; rows
+        // past `xrows` hold stale LDS and are never stored, so they are not
+        // looked at).
+        bool redo[4];
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            redo[i] = 4 * grp + i < xrows && !__builtin_isfinite(acc[i]);
+            any |= redo[i];
+        }
+        if (__builtin_amdgcn_ballot_w64(any) != 0) {   // wave-uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (!redo[i]) continue;
+                float a = acc_in[i];
+                const _Float16 *xr = reinterpret_cast<const _Float16 *>(xbuf + (4 * grp + i) * kXRow);
+#pragma unroll 1
+                for (uint32_t j = 0; j < nb; ++j) {
+                    const uint8_t *blk = region + scale_base + kBytes * j;
+                    const uint16_t sb = (uint16_t)(blk[0] | (blk[1] << 8));
+                    // this kernel keeps Q4 sums in units of 2^-20 (exact: x 16)
+                    a = __builtin_fmaf((float)__builtin_bit_cast(_Float16, sb),
+                                       exact_block<kQ8>(blk + 2, xr + 32 * j) * (kQ8 ? 1.0f : 16.0f), a);
+                }
+                acc[i] = a;
+            }
         }
         // this wave's region is rewritten next: its reads come first
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -689,9 +767,13 @@ hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t r
 template <bool kQ8>
 hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows,
                         size_t in, size_t out, hipStream_t s) {
+    // The vector kernels launch up to 64 work-items per output row (the
+    // one-row GEMV: a 4-wave block per 4 rows); out * 64 must stay below
+    // 2^32, the dispatch packet's work-item count. Past that (2^26 output
+    // rows) the scalar kernel takes the call.
     const bool vector_path = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                              reinterpret_cast<uintptr_t>(w) % 4 == 0 && in <= 0xffffffffu &&
-                             out <= 0xffffffffu;
+                             out <= 0xffffffffu / kWave;
     if (!vector_path) {
         const size_t n = rows * out;
         const size_t blocks = (n + kBlock - 1) / kBlock;

@@ -81,13 +81,25 @@ def arbitrated(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, ulps) -> np.
     return within | closer
 
 
-def rope_close(got, want, src):
+def rope_close(got, want, src, what="RoPE"):
     """RoPE f16 rule: 1 f16 ulp, or -- where l*c - r*s cancels -- the f32
     error of a rotation whose cos/sin are each within an f32 ulp of the
-    reference's: 2^-22 (|l| + |r|)."""
+    reference's: 2^-22 (|l| + |r|).
+
+    Returns (elements, within 1 ulp, passing only through the cancellation
+    clause, largest ulp distance among those) and prints it, so that a
+    widening of the second clause cannot hide behind it."""
     half = src.shape[-1] // 2
     pair = np.abs(src[..., :half].astype(np.float64)) + np.abs(src[..., half:].astype(np.float64))
     pair = np.concatenate([pair, pair], axis=-1)
     d = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    ok = (f16_ulps(got, want) <= 1) | (d <= 2.0 ** -22 * pair)
+    ulps = f16_ulps(got, want)
+    near = ulps <= 1
+    cancel = ~near & (d <= 2.0 ** -22 * pair)
+    ok = near | cancel
+    worst = int(ulps[cancel].max()) if cancel.any() else 0
+    counts = (int(ok.size), int(near.sum()), int(cancel.sum()), worst)
+    print(f"{what}: {counts[0]} elements, {counts[1]} within 1 ulp, {counts[2]} only through "
+          f"the cancellation clause (largest distance there {worst} ulp)", flush=True)
     assert ok.all(), f"{(~ok).sum()} elements beyond the RoPE bound"
+    return counts

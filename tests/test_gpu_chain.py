@@ -37,6 +37,8 @@ def test_config5_chain_full_size(sdk, orc):
     assert_bits_equal(th.download(), h_ref, "residual sum")
     assert_f16_ulps(tn.download(), n_ref, 1, "RMSNorm of the sum")
     q_ref, k_ref = orc.rope(q, k, heads, heads, dim, 10000.0)
-    rope_close(tq.download(), q_ref, q)
-    rope_close(tk.download(), k_ref, k)
+    # the cancellation clause must stay a rare exception at the full shape
+    for name, got, want, src in (("q", tq, q_ref, q), ("k", tk, k_ref, k)):
+        total, _, cancel, _ = rope_close(got.download(), want, src, f"RoPE {name} [4096,32,64]")
+        assert cancel <= total // 10000, f"RoPE {name}: {cancel} of {total} pass only by cancellation"
     assert_f16_ulps(to.download(), orc.silu_multiply(gate, up), 1, "SwiGLU [4096, 8192]")

@@ -327,6 +327,49 @@ def test_quantized_linear(sdk, orc, fmt, shape):
           orc.linear_quant_abs_weight(x, packed, fmt == 1), "f16", f"{name} {shape}")
 
 
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("shape", [(1, 2080, 96), (1, 10336, 9), (2, 1056, 40), (4, 4128, 70),
+                                   (16, 2080, 33), (20, 1056, 130)])
+def test_quantized_linear_non_finite(sdk, orc, fmt, shape):
+    """+-Inf and NaN in x follow the reference's sum of x * (scale q)
+    (tensor_compute_cuda.cu:216-238): +-Inf where every non-finite x meets a
+    non-zero weight and the infinities agree in sign, NaN for a zero weight
+    (Inf * 0), opposite infinities or a NaN input. Shapes cover the split
+    one-row GEMV (an Inf in a partial last chunk, whose lanes past the end
+    read that block's x), the two-row GEMV and the MFMA kernel (a 20-row
+    input leaves a 4-row second tile). Rows with finite x keep the usual
+    bound."""
+    rows, inw, out = shape
+    x = orc.normal((rows, inw), 69, 0, 0.0, 1.0, "f16").copy()
+    w = orc.normal((out, inw), 69, 1, 0.0, 1.0, "f16").copy()
+    planted = {0: [(inw - 5, np.inf)]}
+    if rows > 1:
+        planted[1] = [(3, -np.inf)]
+    if rows > 2:
+        planted[2] = [(40, np.inf), (41, -np.inf)]
+    if rows > 3:
+        planted[rows - 1] = [(inw // 2, np.nan)]
+    for r, cells in planted.items():
+        for k, value in cells:
+            x[r, k] = value
+    w[: min(out, 6) : 5, inw - 5] = 0.0   # Inf * 0 in row 0
+    w[1 % out, 3] = 0.0
+    packed = orc.quantize(w, fmt)
+    y = sdk.tensor("f16", (rows, out))
+    name = "tensor_linear_q8_0_f16" if fmt == 1 else "tensor_linear_q4_0_f16"
+    sdk.call(name, sdk.from_numpy(x), sdk.from_numpy(packed, dtype="u8"), y)
+    got = y.download().astype(np.float64)
+    want = orc.linear_quant(x, packed, fmt == 1).astype(np.float64)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(got), cls(want)), f"{name} {shape}: {cls.__name__} pattern"
+    assert np.isnan(want).any() and np.isinf(want).any(), "the case must produce both outcomes"
+    finite = [r for r in range(rows) if r not in planted]
+    if finite:
+        xf = x[finite]
+        check(got[finite].astype(np.float16), want[finite].astype(np.float16),
+              orc.linear_quant_abs_weight(xf, packed, fmt == 1), "f16", f"{name} {shape} finite rows")
+
+
 def test_quantized_linear_reference_check(sdk, orc):
     """tests/test_tensor_quant.c:62-83 on the device path."""
     w = (((np.arange(64) % 32) - 16).astype(np.float32) / 8).astype(np.float16).reshape(2, 32)

@@ -200,3 +200,24 @@ def test_quantized_linear_reference_check(orc):
         got = orc.linear_quant(x, packed, fmt == 1).astype(np.float32)
         expected = dequant_exact(x, packed, fmt == 1)
         assert np.abs(got - expected).max() <= 0.02
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_quantized_linear_non_finite_closed_form(orc, fmt):
+    """x = +-Inf / NaN through the fmaf chain: IEEE rules fix every output.
+    One block, weights w_k = (k - 12) / 8 quantized (so q_12 = 0): an Inf at
+    k = 12 meets a zero weight (NaN); an Inf at k = 20 gives the sign of x
+    times the sign of its weight; +Inf at 20 and 21 (weights of one sign)
+    stays +Inf; +Inf at 20 and -Inf at 21 is NaN; a NaN anywhere is NaN."""
+    w = ((np.arange(32) - 12) / 8).astype(np.float16).reshape(1, 32)
+    packed = orc.quantize(w, fmt)
+    cases = [({12: np.inf}, "nan"), ({20: np.inf}, "+inf"), ({20: -np.inf}, "-inf"),
+             ({4: np.inf}, "-inf"), ({20: np.inf, 21: np.inf}, "+inf"),
+             ({20: np.inf, 21: -np.inf}, "nan"), ({7: np.nan}, "nan")]
+    for cells, expect in cases:
+        x = np.full((1, 32), 0.5, np.float16)
+        for k, v in cells.items():
+            x[0, k] = v
+        y = float(orc.linear_quant(x, packed, fmt == 1)[0, 0])
+        got = "nan" if np.isnan(y) else ("+inf" if y == np.inf else "-inf" if y == -np.inf else "finite")
+        assert got == expect, (fmt, cells, y)
