@@ -878,6 +878,8 @@ def main():
                     help="only time single-launch copies at 67/134/268 MB: the library's copy, "
                          "hipMemcpyAsync and run-time-compiled copy kernels (1/2/4 vectors per "
                          "lane), one JSON line each")
+    ap.add_argument("--lib", default=None,
+                    help="path of the HIP library to load (default: the in-tree build)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run the counter-collection workload (a calibration copy, then "
                          "every step and suite kernel at its BASELINE shape)")
@@ -890,7 +892,7 @@ def main():
         sys.exit(2)
 
     from inference_c_amd import Sdk
-    sdk = Sdk()
+    sdk = Sdk(args.lib) if args.lib else Sdk()
     sdk.require_device()
     if args.pmc_probe:
         pmc_probe(sdk)
