@@ -149,29 +149,56 @@ __device__ inline void gemv_block(const uint8_t *chunk, uint32_t off, const Gemv
     }
 }
 
-// 2^-24 * sum_k x_k w_k of one block, decoded value by value with the signed
-// weights (the reference's own decode, tensor_compute_cuda.cu:229-234). The
-// path for a block whose x holds an infinity or NaN: the offset decode forms
-// x (w + offset) - offset x, which turns x = +-Inf into Inf - Inf = NaN where
-// the reference's x * (scale w) gives +-Inf (NaN only for w = 0 or mixed
-// signs). `values` are the block's value bytes, `x` its 32 f16 (global
-// memory or LDS). A rolled loop over memory operands: it runs only for
-// non-finite input and adds no registers to the kernels' common path.
+// One output by the reference's own chain (tensor_compute_cuda.cu:216-238):
+// sum = fmaf(x_k, scale_b * q_k, sum) over the blocks b of the row, then the
+// 32 values k of each, from 0. The fix-up for an output whose fast sum is
+// not finite. Finite x and finite scales keep every partial sum of the fast
+// kernels finite (at most ~2^30 for f16 operands), and a non-finite x makes
+// the reference's sum non-finite too, but the offset decode forms
+// x (q + offset) - offset x, so x = +-Inf gives Inf - Inf = NaN where the
+// reference's x * (scale q) gives +-Inf (NaN only for q = 0, a zero scale
+// or infinities of both signs). Running the reference's chain for those
+// outputs makes them equal to the reference's bit for bit. `xrow` is the
+// input row (16-byte aligned), `wrow` the packed weight row (2-byte
+// aligned). Rare: only rows with an infinity or NaN take it.
 template <bool kQ8>
-__device__ inline float exact_block(const uint8_t *values, const _Float16 *x) {
-    float s = 0.0f;
+__device__ inline float reference_chain(const uint16_t *xrow, const uint8_t *wrow,
+                                        uint32_t blocks) {
+    constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
+    float sum = 0.0f;
 #pragma unroll 1
-    for (int k = 0; k < 32; ++k) {
-        int q;
-        if constexpr (kQ8) {
-            q = (int)(int8_t)values[k];
-        } else {
-            const uint8_t packed = values[k & 15];
-            q = (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
+    for (uint32_t b = 0; b < blocks; ++b) {
+        const uint16_t *blk = reinterpret_cast<const uint16_t *>(wrow + (uint64_t)b * kBytes);
+        uint16_t half_words[kBytes / 2];
+#pragma unroll
+        for (uint32_t i = 0; i < kBytes / 2; ++i) half_words[i] = blk[i];
+        const u32x4 *xp = reinterpret_cast<const u32x4 *>(xrow + (uint64_t)b * 32);
+        uint32_t xw[16];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const u32x4 t = xp[v];
+            xw[4 * v] = t.x;
+            xw[4 * v + 1] = t.y;
+            xw[4 * v + 2] = t.z;
+            xw[4 * v + 3] = t.w;
         }
-        s = __builtin_fmaf((float)x[k], (float)q * 0x1p-24f, s);
+        const float scale = (float)__builtin_bit_cast(_Float16, half_words[0]);
+#pragma unroll
+        for (uint32_t k = 0; k < 32; ++k) {
+            int q;
+            if constexpr (kQ8) {
+                const uint32_t byte = k;   // value byte k sits at block byte 2 + k
+                q = (int)(int8_t)(uint8_t)(half_words[1 + byte / 2] >> (8 * (byte & 1)));
+            } else {
+                const uint32_t byte = k & 15;
+                const uint8_t packed = (uint8_t)(half_words[1 + byte / 2] >> (8 * (byte & 1)));
+                q = (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
+            }
+            const uint16_t xb = (uint16_t)(xw[k / 2] >> (16 * (k & 1)));
+            sum = __builtin_fmaf((float)__builtin_bit_cast(_Float16, xb), scale * (float)q, sum);
+        }
     }
-    return s;
+    return sum;
 }
 
 // Grid: x = waves of O output rows (4 waves per block), y = groups of R
@@ -253,7 +280,6 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         const uint32_t b = c0 + min(lane, nb - 1);
         uint32_t xv[R][16];
         float base[R];   // -offset * 2^-24 * (the x sum of the lane's block)
-        bool nonfinite[R];   // the block's x holds an infinity or NaN
         const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -272,16 +298,9 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
                 xs0 = __builtin_amdgcn_fdot2(as_half2(xv[r][i]), one2, xs0, false);
                 xs1 = __builtin_amdgcn_fdot2(as_half2(xv[r][i + 1]), one2, xs1, false);
             }
-            // -offset * 2^-24 * sum (exact: a power of two times the sum).
-            // 32 finite f16 sum to at most 2^21 in magnitude, so the sum is
-            // non-finite exactly when one of them is.
+            // -offset * 2^-24 * sum (exact: a power of two times the sum)
             base[r] = (xs0 + xs1) * (kQ8 ? -0x1p-17f : -0x1p-21f);
-            nonfinite[r] = !__builtin_isfinite(xs0 + xs1);
         }
-        bool any = false;
-#pragma unroll
-        for (int r = 0; r < R; ++r) any |= nonfinite[r];
-        const bool redo = __builtin_amdgcn_ballot_w64(any) != 0;   // wave-uniform
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
@@ -303,20 +322,9 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
             float dot[R];
             gemv_block<kQ8, R>(region[o], off, (lead[o] & 2u) ? sel_lead2 : sel_lead0, xv, base, scale,
                                dot);
-            if (redo) {
-                // rare: a non-finite x in some lane's block. Those blocks are
-                // recomputed with the signed decode; a lane past the chunk's
-                // end (whose x is the last block's, possibly non-finite) adds 0
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    if (!live) dot[r] = 0.0f;
-                    else if (nonfinite[r])
-                        dot[r] = exact_block<kQ8>(region[o] + off + 2,
-                                                  reinterpret_cast<const _Float16 *>(xrow[r]) +
-                                                      (uint64_t)b * 32);
-                }
-            }
-            // a lane past the chunk's end adds 0 * (a finite dot)
+            // a lane past the chunk's end adds 0 * (its dot: finite unless
+            // the chunk's last block of x holds an infinity or NaN, and then
+            // the row's output is redone below)
             const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(live ? scale : 0u));
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[o][r] = __builtin_fmaf((float)sc, dot[r], acc[o][r]);
@@ -324,15 +332,16 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
-    // sums are kept as 2^-24 times the dot products until here (exact)
+    // sums are kept as 2^-24 times the dot products until here (exact). An
+    // output whose sum is not finite is redone by the reference's chain.
     if constexpr (kSplit) {
         __shared__ float part[kWaves][O * R];
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const float total = wave_sum(acc[o][r]);
-                if (lane == 0) part[kpart][o * R + r] = total;
+                const float t = wave_sum(acc[o][r]);
+                if (lane == 0) part[kpart][o * R + r] = t;
             }
         __syncthreads();
         if (threadIdx.x < O * R) {
@@ -340,19 +349,37 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
             float total = 0.0f;
 #pragma unroll
             for (uint32_t k = 0; k < kWaves; ++k) total += part[k][threadIdx.x];
-            if (o0 + o < out && r0 + r < rows)
-                y[(uint64_t)(r0 + r) * out + o0 + o] =
-                    __builtin_bit_cast(uint16_t, (_Float16)(total * 0x1p24f));
+            total *= 0x1p24f;
+            if (o0 + o < out && r0 + r < rows) {
+                if (!__builtin_isfinite(total))
+                    total = reference_chain<kQ8>(x + (uint64_t)(r0 + r) * in,
+                                                 w + (uint64_t)(o0 + o) * row_bytes, blocks);
+                y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+            }
         }
     } else {
+        uint32_t bad = 0;   // wave-uniform: outputs (bit o * R + r) whose sum is not finite
 #pragma unroll
         for (int o = 0; o < O; ++o)
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float total = wave_sum(acc[o][r]) * 0x1p24f;
+                if (!__builtin_isfinite(total)) bad |= 1u << (o * R + r);
                 if (lane == 0 && o0 + o < out && r0 + r < rows)
                     y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
             }
+        // rare; one output at a time so the chain is inlined once
+#pragma unroll 1
+        while (bad != 0) {
+            const uint32_t j = (uint32_t)__builtin_ctz(bad);
+            bad &= bad - 1;
+            const uint32_t o = j / R, r = j % R;
+            if (lane == 0 && o0 + o < out && r0 + r < rows) {
+                const float total = reference_chain<kQ8>(x + (uint64_t)(r0 + r) * in,
+                                                         w + (uint64_t)(o0 + o) * row_bytes, blocks);
+                y[(uint64_t)(r0 + r) * out + o0 + o] = __builtin_bit_cast(uint16_t, (_Float16)total);
+            }
+        }
     }
 }
 
@@ -579,44 +606,12 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(scale, d[i], acc[i]);
         };
-        const f32x4 acc_in = acc;
         if (nb == kChunk) {
             static_for<kChunk>([&](auto jc) { block(jc); });
         } else {
             static_for<kChunk>([&](auto jc) {
                 if ((uint32_t)decltype(jc)::value < nb) block(jc);
             });
-        }
-        // A row whose x holds an infinity or NaN in this chunk: the offset
-        // MFMA turns x * w into x * (w + offset) - offset * x, NaN for
-        // x = +-Inf where the reference gives +-Inf. Finite x keeps every
-        // partial finite, so a live row whose sum turned non-finite here is
-        // redone from the chunk's start with the signed decode (rare; rows
-        // past `xrows` hold stale LDS and are never stored, so they are not
-        // looked at).
-        bool redo[4];
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            redo[i] = 4 * grp + i < xrows && !__builtin_isfinite(acc[i]);
-            any |= redo[i];
-        }
-        if (__builtin_amdgcn_ballot_w64(any) != 0) {   // wave-uniform
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (!redo[i]) continue;
-                float a = acc_in[i];
-                const _Float16 *xr = reinterpret_cast<const _Float16 *>(xbuf + (4 * grp + i) * kXRow);
-#pragma unroll 1
-                for (uint32_t j = 0; j < nb; ++j) {
-                    const uint8_t *blk = region + scale_base + kBytes * j;
-                    const uint16_t sb = (uint16_t)(blk[0] | (blk[1] << 8));
-                    // this kernel keeps Q4 sums in units of 2^-20 (exact: x 16)
-                    a = __builtin_fmaf((float)__builtin_bit_cast(_Float16, sb),
-                                       exact_block<kQ8>(blk + 2, xr + 32 * j) * (kQ8 ? 1.0f : 16.0f), a);
-                }
-                acc[i] = a;
-            }
         }
         // this wave's region is rewritten next: its reads come first
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -626,14 +621,26 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
     const uint32_t o = o0 + col;
     const float unit = kQ8 ? 16777216.0f : 1048576.0f;   // 2^24, 2^20
 #pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= unit;
+    // an output whose sum is not finite (its x row holds an infinity or NaN)
+    // is redone by the reference's chain, one (row, output) at a time so the
+    // chain is inlined once
+#pragma unroll 1
     for (int i = 0; i < 4; ++i) {
         const uint32_t r = r0 + 4 * grp + i;
-        if (r < rows && o < out)
-            y[(uint64_t)r * out + o] = __builtin_bit_cast(uint16_t, (_Float16)(acc[i] * unit));
+        if (r >= rows || o >= out) continue;
+        float v = acc[0];
+        v = i == 1 ? acc[1] : v;
+        v = i == 2 ? acc[2] : v;
+        v = i == 3 ? acc[3] : v;
+        if (!__builtin_isfinite(v))
+            v = reference_chain<kQ8>(x + (uint64_t)r * in, w + (uint64_t)o * row_bytes, blocks);
+        y[(uint64_t)r * out + o] = __builtin_bit_cast(uint16_t, (_Float16)v);
     }
 }
 
-// Any alignment: one thread per output, bytes read one at a time.
+// Any alignment: one thread per output, bytes read one at a time, the
+// reference's chain (tensor_compute_cuda.cu:216-238) operation for operation.
 template <bool kQ8>
 __global__ __launch_bounds__(kBlock) void quant_linear_scalar_kernel(const uint16_t *__restrict__ x,
                                                                      const uint8_t *__restrict__ w,
@@ -649,7 +656,6 @@ __global__ __launch_bounds__(kBlock) void quant_linear_scalar_kernel(const uint1
     for (uint32_t b = 0; b < blocks; ++b) {
         const uint8_t *blk = base + (uint64_t)b * Fmt<kQ8>::kBytes;
         const float scale = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8)));
-        float part = 0.0f;
         for (uint32_t k = 0; k < 32; ++k) {
             int v;
             if constexpr (kQ8) {
@@ -659,9 +665,8 @@ __global__ __launch_bounds__(kBlock) void quant_linear_scalar_kernel(const uint1
                 v = (int)(k < 16 ? packed & 15 : packed >> 4) - 8;
             }
             const float xv = (float)__builtin_bit_cast(_Float16, x[r * in + b * 32 + k]);
-            part = __builtin_fmaf(xv, (float)v, part);
+            sum = __builtin_fmaf(xv, scale * (float)v, sum);
         }
-        sum = __builtin_fmaf(scale, part, sum);
     }
     y[i] = __builtin_bit_cast(uint16_t, (_Float16)sum);
 }

@@ -430,4 +430,6 @@ def test_quantized_slots(sdk, orc, fmt):
     ty2 = sdk.tensor("f16", (rows, out))
     assert dev(tx2.device_ptr() + 2, tw2.device_ptr() + 2, ty2.device_ptr(), rows, inw, out)
     check(ty2.download(), want, weight, "f16", "device slot, unaligned")
+    # the scalar kernel runs the reference's chain operation for operation
+    assert_bits_equal(ty2.download(), want, "device slot, unaligned: the reference's chain")
     assert dev(tx.device_ptr(), tw.device_ptr(), ty.device_ptr(), 0, inw, out) == 0

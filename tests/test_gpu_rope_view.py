@@ -30,6 +30,43 @@ def test_rope_f16(sdk, orc, seq, qh, kh, dim, offset, device):
     rope_close(tk.download(), wk, k)
 
 
+# Shapes of the 1 KB-group path (half a row a whole number of 16-byte vectors,
+# a power of two of them, and heads x vectors a multiple of 32 in both
+# tensors): 1, 2, 4 and 8 groups per wave, positions of 1, 2, 4 and 8
+# groups, more q blocks than k blocks and the reverse, and ragged tensors
+# whose last waves hold groups past the end.
+GROUP_SHAPES = [
+    ("f16", 3, 16, 8, 64, 0),          # 1 group per wave, dead waves and groups
+    ("f16", 70, 32, 64, 16, 2),        # one vector per half row
+    ("f16", 300, 16, 32, 32, 9),       # two vectors per half row
+    ("f16", 700, 2, 4, 256, 0),        # 16 vectors per half row
+    ("f16", 4001, 8, 16, 64, 11),      # 2 groups per wave, k has twice q's blocks
+    ("f16", 1501, 32, 16, 128, 77),    # 4 groups per wave, 2 positions per wave
+    ("f16", 20001, 8, 8, 64, 1 << 20),  # 8 groups per wave over 8 positions
+    ("f32", 64, 8, 4, 64, 3),
+    ("f32", 33, 1, 1, 256, 0),         # 32 vectors per half row
+    ("f32", 4096, 32, 8, 64, 0),       # 8 groups per wave, q has 4x k's blocks
+]
+
+
+@pytest.mark.parametrize("dtype,seq,qh,kh,dim,offset", GROUP_SHAPES)
+def test_rope_group_path(sdk, orc, dtype, seq, qh, kh, dim, offset):
+    q = orc.normal((seq, qh, dim), 52, 0, 0.0, 1.0, dtype)
+    k = orc.normal((seq, kh, dim), 52, 1, 0.0, 1.0, dtype)
+    tq, tk = sdk.from_numpy(q), sdk.from_numpy(k)
+    sdk.call(f"tensor_rope_{dtype}", tq, tk, qh, kh, dim, 10000.0, offset)
+    wq, wk = orc.rope(q, k, qh, kh, dim, 10000.0, offset)
+    if dtype == "f16":
+        rope_close(tq.download(), wq, q)
+        rope_close(tk.download(), wk, k)
+        return
+    half = dim // 2
+    for got, want, src in ((tq.download(), wq, q), (tk.download(), wk, k)):
+        mag = np.sqrt(src[..., :half] ** 2 + src[..., half:] ** 2)
+        mag = np.concatenate([mag, mag], axis=-1)
+        assert np.all(np.abs(got - want) <= 2e-6 * mag + 1e-30)
+
+
 @pytest.mark.parametrize("seq,qh,kh,dim,offset", [(64, 4, 2, 64, 0), (7, 3, 3, 10, 77),
                                                    (2, 150, 150, 64, 3), (45, 3, 1, 8, 9)])
 def test_rope_f32(sdk, orc, seq, qh, kh, dim, offset):
