@@ -11,9 +11,11 @@ once, each output written once) over the wall time of K steps run back to
 back. A second pass of K steps with HIP events on the SDK stream (the stream
 the kernels run on) at each step's start and at the end of its chain gives
 the chain's and the global reduction's average durations; the dominant call,
-the global sum/max (4 GiB read), against the 8 TB/s HBM peak is `roofline`. The 4 GiB read of every step evicts the
-chain's operands from the 256 MB last-level cache, so each step's chain
-starts from HBM.
+the global sum/max (4 GiB read), against the 8 TB/s HBM peak is `roofline`.
+The chain's operands come in three copies used in turn, so at least 600 MB
+of other chain traffic (besides the 4 GiB read) separates two uses of one
+copy and each step's chain starts from HBM, not the 256 MB last-level
+cache.
 
 The other BASELINE configs (configs[1]'s SiLU/GELU/SwiGLU among them) are
 timed per kernel and reported under "suite". `cpu_baseline` times the
@@ -57,6 +59,9 @@ CFG5 = {
 # the elements the benchmark definition counts for the chain's elements/s
 # (2720 G/s at 80% of the HBM peak, i.e. over 52.43 us)
 CFG5_CHAIN_ELEMENTS = 142_606_336
+# copies of the chain's operands the step uses in turn (302 MB each with
+# its outputs: two others, 604 MB, between two uses of one copy)
+CHAIN_SETS = 3
 
 
 class Hip:
@@ -903,8 +908,13 @@ def main():
     hip = Hip()
     stream = sdk.stream()
 
-    # configs[4] operands, seed 5 (chain) and seed 0 (global), one set: the
-    # step's 4 GiB global read flushes the last-level cache between chains.
+    # configs[4] operands, seed 5 (chain) and seed 0 (global). The chain's
+    # operands (302 MB with its outputs) come in CHAIN_SETS copies used in
+    # turn, so at least 600 MB of other chain traffic separates two uses of
+    # one copy and no step's chain can find the previous step's operands in
+    # the 256 MB last-level cache, whatever the global reduction's
+    # non-temporal 4 GiB read leaves there. The global input is one 4 GiB
+    # buffer (16 x the cache).
     tok, hid, inter = 4096, 2048, 8192
 
     def filled(dtype, shape, kind, seed, stream_id, a, b):
@@ -912,29 +922,38 @@ def main():
         sdk.call("tensor_fill_" + kind, x, seed, stream_id, a, b)
         return x
 
-    t = {"x": filled("f16", (tok, hid), "normal", 5, 0, 0.0, 1.0),
-         "r": filled("f16", (tok, hid), "normal", 5, 1, 0.0, 1.0),
-         "w": filled("f16", (hid,), "normal", 5, 9, 0.0, 1.0),
-         "h": sdk.tensor("f16", (tok, hid)), "n": sdk.tensor("f16", (tok, hid)),
-         "q": filled("f16", (tok, 32, 64), "normal", 5, 2, 0.0, 1.0),
-         "k": filled("f16", (tok, 32, 64), "normal", 5, 3, 0.0, 1.0),
-         "g": filled("f16", (tok, inter), "normal", 5, 4, 0.0, 1.0),
-         "u": filled("f16", (tok, inter), "normal", 5, 5, 0.0, 1.0),
-         "o": sdk.tensor("f16", (tok, inter)),
-         "big": filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0),
+    def chain_set():
+        return {"x": filled("f16", (tok, hid), "normal", 5, 0, 0.0, 1.0),
+                "r": filled("f16", (tok, hid), "normal", 5, 1, 0.0, 1.0),
+                "w": filled("f16", (hid,), "normal", 5, 9, 0.0, 1.0),
+                "h": sdk.tensor("f16", (tok, hid)), "n": sdk.tensor("f16", (tok, hid)),
+                "q": filled("f16", (tok, 32, 64), "normal", 5, 2, 0.0, 1.0),
+                "k": filled("f16", (tok, 32, 64), "normal", 5, 3, 0.0, 1.0),
+                "g": filled("f16", (tok, inter), "normal", 5, 4, 0.0, 1.0),
+                "u": filled("f16", (tok, inter), "normal", 5, 5, 0.0, 1.0),
+                "o": sdk.tensor("f16", (tok, inter))}
+
+    sets = [chain_set() for _ in range(CHAIN_SETS)]
+    g = {"big": filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0),
          "sum": sdk.tensor("f64", (1,)), "max": sdk.tensor("f32", (1,))}
     sdk.synchronize()
-    calls = [
-        ("cfg5_residual_rms_norm_f16", lambda: sdk.call("tensor_residual_rms_norm_f16", t["x"], t["r"],
-                                                   t["w"], 1e-6, t["h"], t["n"])),
-        ("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", t["q"], t["k"], 32, 32, 64, 10000.0, 0)),
-        # out = up * silu(gate): the compute-table order, gate first
-        ("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["g"], t["u"], t["o"])),
-        ("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", t["big"], t["sum"],
-                                                t["max"])),
-    ]
-    for _ in range(args.warmup):
-        for _, fn in calls:
+
+    def step_calls(t):
+        return [
+            ("cfg5_residual_rms_norm_f16", lambda: sdk.call("tensor_residual_rms_norm_f16", t["x"],
+                                                       t["r"], t["w"], 1e-6, t["h"], t["n"])),
+            ("cfg5_rope_f16", lambda: sdk.call("tensor_rope_f16", t["q"], t["k"], 32, 32, 64,
+                                               10000.0, 0)),
+            # out = up * silu(gate): the compute-table order, gate first
+            ("cfg5_swiglu_f16", lambda: sdk.call("tensor_silu_multiply_f16", t["g"], t["u"], t["o"])),
+            ("cfg5_global_sum_max_f32", lambda: sdk.call("tensor_sum_max_f32", g["big"], g["sum"],
+                                                    g["max"])),
+        ]
+
+    steps = [step_calls(t) for t in sets]   # step i runs steps[i % CHAIN_SETS]
+    calls = steps[0]
+    for i in range(args.warmup):
+        for _, fn in steps[i % CHAIN_SETS]:
             fn()
     sdk.synchronize()
     # Timed region: K steps back to back on the SDK stream, synchronised on
@@ -944,8 +963,8 @@ def main():
     begin, end = hip.event(), hip.event()
     t0 = time.perf_counter()
     hip.record(begin, stream)
-    for _ in range(args.steps):
-        for _, fn in calls:
+    for i in range(args.steps):
+        for _, fn in steps[i % CHAIN_SETS]:
             fn()
     hip.record(end, stream)
     sdk.synchronize()
@@ -959,18 +978,19 @@ def main():
     marks = [hip.event() for _ in range(2 * args.steps + 1)]
     for i in range(args.steps):
         hip.record(marks[2 * i], stream)
-        for _, fn in calls[:3]:
+        for _, fn in steps[i % CHAIN_SETS][:3]:
             fn()
         hip.record(marks[2 * i + 1], stream)
-        calls[3][1]()
+        steps[i % CHAIN_SETS][3][1]()
     hip.record(marks[-1], stream)
     sdk.synchronize()
     chain_ms = statistics.fmean(hip.elapsed_ms(marks[2 * i], marks[2 * i + 1])
                                 for i in range(args.steps))
     global_ms = statistics.fmean(hip.elapsed_ms(marks[2 * i + 1], marks[2 * i + 2])
                                  for i in range(args.steps))
-    for v in t.values():
-        v.free()
+    for t in sets + [g]:
+        for v in t.values():
+            v.free()
 
     step_bytes = sum(v[0] for v in CFG5.values())
     step_elems = CFG5_CHAIN_ELEMENTS + CFG5["cfg5_global_sum_max_f32"][1]
@@ -1000,6 +1020,7 @@ def main():
                                "[4096,8192]; all N(0,1), seed 5) then the global sum + max over "
                                "2^30 f32 U[-1,1] (seed 0); inputs resident in HBM",
                    "step_bytes": step_bytes, "elements_per_step": step_elems,
+                   "chain_operand_sets": CHAIN_SETS,
                    "dtypes": "chain f16 (f32 arithmetic), global f32 (f64 sum)"},
         "pct_of_peak": round(100 * value / PEAK_GBPS, 1),
         "elements_per_s": float(f"{step_elems / (ms_per_step * 1e-3):.4g}"),
