@@ -77,7 +77,8 @@ def arbitrated(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, ulps) -> np.
     within = ulps(got, ref) <= 1
     g = got.astype(np.float64)
     r = ref.astype(np.float64)
-    closer = np.abs(g - exact) <= np.abs(r - exact)
+    with np.errstate(invalid="ignore"):   # Inf - Inf: NaN compares False; `within` decides
+        closer = np.abs(g - exact) <= np.abs(r - exact)
     return within | closer
 
 
