@@ -311,12 +311,17 @@ def _cpu_counts():
 # ---- per-config kernel suite ------------------------------------------------
 
 ROTATE_BYTES = 600 << 20  # traffic between two uses of the same buffers (> 256 MB MALL)
+BATCH_MS = 3.0            # GPU time per timed batch of the suite (sustained clocks)
+MAX_BATCH_LAUNCHES = 400
+WARM_MS = 20.0            # untimed GPU time before an entry's timed batches
 
 
-def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
-    """Each BASELINE config's kernels: `reps` back-to-back launches between
-    two events on the SDK stream, average per launch; the best of `rounds`
-    such batches is reported with all of them. Every launch rotates to the
+def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
+    """Each BASELINE config's kernels: batches of at least `reps`
+    back-to-back launches and at least BATCH_MS of GPU time (up to
+    MAX_BATCH_LAUNCHES) between two events on the SDK stream, average per
+    launch; the median of `rounds` such batches is the reported time
+    (`avg_us`), with the best (`best_us`) and all of them (`batches_us`). Every launch rotates to the
     next of enough identical copies of its operands that >= 600 MB of other
     traffic separates two uses of the same bytes, so no operand is served
     from the 256 MB last-level cache. Beside each kernel, a plain contiguous
@@ -344,13 +349,25 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
         for i in range(warmup):
             run(sets[i % copies])
         start, stop = hip.event(), hip.event()
-        batches = []
-        for _ in range(rounds):
+
+        def batch(n):
             hip.record(start, stream)
-            for i in range(reps):
+            for i in range(n):
                 run(sets[i % copies])
             hip.record(stop, stream)
-            batches.append(hip.elapsed_ms(start, stop) / reps)
+            return hip.elapsed_ms(start, stop) / n
+        # A batch lasts at least BATCH_MS of GPU time (sized from a first,
+        # untimed batch of `reps`), after WARM_MS of untimed launches: the
+        # GPU's power management lowers the core clock whenever it idles
+        # (between short batches, during an entry's set-up) and raises it
+        # again over ~15 ms of load, which moves the kernels that depend on
+        # it (the quantized GEMVs by up to 25%, attention and the hipBLASLt
+        # GEMM by 10-20%) and not the memory-bound ones.
+        per_launch = max(batch(reps), 1e-4)
+        n = max(reps, min(MAX_BATCH_LAUNCHES, int(BATCH_MS / per_launch) + 1))
+        for i in range(int(WARM_MS / per_launch) + 1):
+            run(sets[i % copies])
+        batches = [batch(n) for _ in range(rounds)]
         del sets
         sdk.synchronize()
         return batches, copies
@@ -358,7 +375,7 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
     copy_floor = {}
 
     def copy_us(alg_bytes):
-        """Best time of a plain contiguous f16 copy moving the same bytes
+        """Median time of a plain contiguous f16 copy moving the same bytes
         (alg_bytes / 2 read, alg_bytes / 2 written): what one launch of this
         size reaches on this device, launch and drain included."""
         if alg_bytes not in copy_floor:
@@ -368,31 +385,31 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
                                         T("f16", (n,))),
                                lambda c: sdk.call("tensor_view_add_mul_f16", c[0], view, None,
                                                   None, c[1]), alg_bytes)
-            copy_floor[alg_bytes] = min(batches)
+            copy_floor[alg_bytes] = statistics.median(batches)
         return copy_floor[alg_bytes]
 
     def measure(name, make_set, run, alg_bytes, elements):
         if not wanted(name):
             return
         batches, copies = timed(make_set, run, alg_bytes)
-        best = min(batches)
+        med = statistics.median(batches)   # the reported time: the median batch
         floor = copy_us(alg_bytes)
-        results[name] = {"avg_us": round(best * 1e3, 2),
+        results[name] = {"avg_us": round(med * 1e3, 2), "best_us": round(min(batches) * 1e3, 2),
                          "batches_us": [round(t * 1e3, 2) for t in batches],
-                         "gbps": round(alg_bytes / (best * 1e-3) / 1e9, 1),
-                         "pct_peak": round(100 * alg_bytes / (best * 1e-3) / 1e9 / PEAK_GBPS, 1),
-                         "elements_per_s": float(f"{elements / (best * 1e-3):.4g}"),
+                         "gbps": round(alg_bytes / (med * 1e-3) / 1e9, 1),
+                         "pct_peak": round(100 * alg_bytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                         "elements_per_s": float(f"{elements / (med * 1e-3):.4g}"),
                          "bytes": alg_bytes, "buffer_sets": copies,
                          "copy_same_bytes_us": round(floor * 1e3, 2),
-                         "pct_of_copy": round(100 * floor / best, 1)}
+                         "pct_of_copy": round(100 * floor / med, 1)}
         traffic = measured_traffic(name)
         if traffic is not None:
             # HBM bytes the kernel actually moved (counter runs): the rate on
             # real traffic, beside the algorithmic figure above
             results[name].update({"traffic_bytes": traffic,
                                   "traffic_over_algorithmic": round(traffic / alg_bytes, 4),
-                                  "gbps_traffic": round(traffic / (best * 1e-3) / 1e9, 1),
-                                  "pct_peak_traffic": round(100 * traffic / (best * 1e-3) / 1e9
+                                  "gbps_traffic": round(traffic / (med * 1e-3) / 1e9, 1),
+                                  "pct_peak_traffic": round(100 * traffic / (med * 1e-3) / 1e9
                                                             / PEAK_GBPS, 1)})
 
     # the host's per-call cost through this Python binding: a 64-element f32
@@ -407,7 +424,7 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
         batches, _ = timed(tiny, lambda s: sdk.call("tensor_add_f32", s[0], s[1], s[2]),
                            ROTATE_BYTES)
         results["host_call_floor_add_f32_64"] = {
-            "avg_us": round(min(batches) * 1e3, 2),
+            "avg_us": round(statistics.median(batches) * 1e3, 2),
             "batches_us": [round(b * 1e3, 2) for b in batches],
             "note": "one-block kernel called back to back from Python: the host's per-call "
                     "cost (the GPU side of the same launch is ~1.2 us)"}
@@ -540,11 +557,12 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
     name_p = "linear_f16_prefill_4096x4096_to_4096_bias"
     if wanted(name_p):
         batches, _ = timed(linear_set(rows_p, in_p, out_p), run_linear, p_bytes)
-        best = min(batches)
+        med = statistics.median(batches)
         results[name_p] = {
-            "avg_us": round(best * 1e3, 2), "batches_us": [round(t * 1e3, 2) for t in batches],
-            "tflops": round(p_flops / (best * 1e-3) / 1e12, 1),
-            "pct_peak_mfma": round(100 * p_flops / (best * 1e-3) / 1e12
+            "avg_us": round(med * 1e3, 2), "best_us": round(min(batches) * 1e3, 2),
+            "batches_us": [round(t * 1e3, 2) for t in batches],
+            "tflops": round(p_flops / (med * 1e-3) / 1e12, 1),
+            "pct_peak_mfma": round(100 * p_flops / (med * 1e-3) / 1e12
                                    / MFMA_PEAK_TFLOPS["f16"], 1),
             "peak_tflops": MFMA_PEAK_TFLOPS["f16"], "flops": p_flops, "bytes": p_bytes,
             "library": "hipBLASLt (bias epilogue)"}
@@ -589,12 +607,12 @@ def suite(sdk, hip, stream, reps=20, rounds=3, only=None):
         batches, copies = timed(make, lambda s: sdk.call(f"tensor_sdpa_device_{dtype}", s[0], s[1],
                                                          s[2], None, 1.0 / d ** 0.5, int(causal),
                                                          s[3]), alg_bytes)
-        best = min(batches)
+        med = statistics.median(batches)
         peak = MFMA_PEAK_TFLOPS[dtype]
-        results[name] = {"avg_us": round(best * 1e3, 2),
+        results[name] = {"avg_us": round(med * 1e3, 2), "best_us": round(min(batches) * 1e3, 2),
                          "batches_us": [round(t * 1e3, 2) for t in batches],
-                         "tflops": round(flops / (best * 1e-3) / 1e12, 1),
-                         "pct_peak_mfma": round(100 * flops / (best * 1e-3) / 1e12 / peak, 1),
+                         "tflops": round(flops / (med * 1e-3) / 1e12, 1),
+                         "pct_peak_mfma": round(100 * flops / (med * 1e-3) / 1e12 / peak, 1),
                          "peak_tflops": peak, "flops": flops, "bytes": alg_bytes,
                          "shape": {"batch": b, "q_heads": hq, "kv_heads": hkv, "q_len": lq,
                                    "kv_len": lk, "head_dim": d, "causal": causal}}
