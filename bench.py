@@ -388,7 +388,24 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
             copy_floor[alg_bytes] = statistics.median(batches)
         return copy_floor[alg_bytes]
 
-    def measure(name, make_set, run, alg_bytes, elements):
+    in_place_floor = {}
+
+    def in_place_copy_us(alg_bytes):
+        """Median time of the same copy with one buffer as both input and
+        output (alg_bytes / 2 read and written back in place): the floor of
+        a kernel that updates its operand in place, such as RoPE. (The copy
+        kernel reads and writes each 16-byte vector in one lane, so the
+        self-copy is well defined.)"""
+        if alg_bytes not in in_place_floor:
+            n = alg_bytes // 4
+            view = TensorView.make((n,), (1,), 0)
+            batches, _ = timed(lambda: (filled("f16", (n,), "normal", 9, 0, 0.0, 1.0),),
+                               lambda c: sdk.call("tensor_view_add_mul_f16", c[0], view, None,
+                                                  None, c[0]), alg_bytes)
+            in_place_floor[alg_bytes] = statistics.median(batches)
+        return in_place_floor[alg_bytes]
+
+    def measure(name, make_set, run, alg_bytes, elements, in_place=False):
         if not wanted(name):
             return
         batches, copies = timed(make_set, run, alg_bytes)
@@ -402,6 +419,10 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
                          "bytes": alg_bytes, "buffer_sets": copies,
                          "copy_same_bytes_us": round(floor * 1e3, 2),
                          "pct_of_copy": round(100 * floor / med, 1)}
+        if in_place:
+            floor_ip = in_place_copy_us(alg_bytes)
+            results[name].update({"copy_in_place_us": round(floor_ip * 1e3, 2),
+                                  "pct_of_in_place_copy": round(100 * floor_ip / med, 1)})
         traffic = measured_traffic(name)
         if traffic is not None:
             # HBM bytes the kernel actually moved (counter runs): the rate on
@@ -500,7 +521,7 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
         swiglu(s)
     measure("cfg5_decoder_chain_f16", cfg5, chain, 335_548_416, 142_606_336)
     measure("cfg5_residual_rms_norm_f16", cfg5, norm, 67_112_960, 8_388_608)
-    measure("cfg5_rope_f16", cfg5, rope, 67_108_864, 16_777_216)
+    measure("cfg5_rope_f16", cfg5, rope, 67_108_864, 16_777_216, in_place=True)
     measure("cfg5_swiglu_f16", cfg5, swiglu, 201_326_592, 33_554_432)
     # embedding gather: a 32768-token prefill batch of int32 ids into
     # a [32000, 2048] f16 table; device storage, so each call also runs the
