@@ -8,8 +8,9 @@ reference would do it.
    include/, src/, tests/ and the one third-party header a source includes
    (third_party/stb_image.h, from src/common/image.c) -- to a scratch
    directory (the reference itself is read-only and is never built in).
-2. Applies the three CMake edits of INTEGRATION.md section 2, read from that
-   file's ```cmake blocks, so the text tested is the text documented:
+2. Applies the three CMake edits documented for maintainers, read from the
+   ```cmake blocks of the integration notes' CMake section (the file named in
+   stanza_blocks), so the text tested is the text documented:
    block 1 replaces the backend check's last line, block 2 goes before the
    closing endif() of the backend if-chain (after the METAL branch), block 3
    after the library's compile definitions.
@@ -39,7 +40,7 @@ DEFINITIONS = ("target_compile_definitions(inference_sdk PUBLIC "
 
 
 def stanza_blocks():
-    """The three ```cmake blocks of INTEGRATION.md section 2, in order."""
+    """The three ```cmake blocks of the integration notes' CMake section, in order."""
     with open(os.path.join(REPO, "INTEGRATION.md")) as f:
         text = f.read()
     start = text.index("## 2. CMake")

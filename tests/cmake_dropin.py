@@ -1,6 +1,6 @@
 """Runs the reference's registered C tests from its own CMake build with
 INFERENCE_SDK_BACKEND=HIP (oracle/cmake_dropin.py builds it into
-oracle/_ref/cmake_hip/, applying INTEGRATION.md's three CMake edits to a
+oracle/_ref/cmake_hip/, applying the maintainers' three CMake edits to a
 scratch copy of the reference). Each test runs through that build's own
 CTest, with the working directory and skip code its CMakeLists.txt:245-317
 registers."""

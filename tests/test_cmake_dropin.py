@@ -1,4 +1,4 @@
-"""The CMake stanza of INTEGRATION.md, without a GPU: the reference built by
+"""The maintainers' HIP CMake stanza, without a GPU: the reference built by
 its own CMake with INFERENCE_SDK_BACKEND=HIP registers its 16 GPU-backend
 tests; the 11 that do no tensor arithmetic pass through CTest, and
 test_tensor_device takes its registered skip code 77. The arithmetic tests run

@@ -1,4 +1,4 @@
-"""The CMake stanza of INTEGRATION.md on the GPU: all 16 tests the reference's
+"""The maintainers' HIP CMake stanza on the GPU: all 16 tests the reference's
 CMakeLists.txt registers for a GPU backend, built by its own CMake with
 INFERENCE_SDK_BACKEND=HIP, pass through CTest (test_tensor_device must run,
 not skip)."""
