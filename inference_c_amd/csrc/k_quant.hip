@@ -10,10 +10,10 @@
 // y[r][o] = f16(sum_b scale_b * sum_k x[r][32b+k] * q_bk).
 //
 // GEMV: a wave works on O output rows in chunks of 64 blocks -- with one
-// input row the block's 4 waves share O rows and take every 4th chunk
-// (their sums meet in LDS: four short waves per block instead of one long
-// one, so a launch has no long last round), with two each wave owns O rows
-// and walks all their chunks.
+// input row (and with two for Q4_0) the block's 4 waves share O rows and
+// take every 4th chunk (their sums meet in LDS: four short waves per block
+// instead of one long one, so a launch has no long last round); with two
+// Q8_0 rows each wave owns O rows and walks all their chunks.
 // Each chunk of each row is a contiguous byte range; the wave reads it with
 // coalesced 16-byte loads (the aligned 16-byte segments covering the range)
 // into its own LDS region, then lane l takes block l of the chunk from LDS:
@@ -789,7 +789,7 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
         return hipGetLastError();
     }
     // One or two input rows: the GEMV, 4 output rows per wave, or per block
-    // of 4 waves splitting the chunks for one row (2, 6 and 8 measured
+    // of 4 waves splitting the chunks (one row; two Q4_0 rows) (2, 6 and 8 measured
     // slower for both formats and both forms), decoding each weight once for the
     // rows. From three rows quant_mma_kernel, which decodes each weight once
     // for up to 16 ([28672, 8192] Q8_0: 2 rows 51 us GEMV vs 56 MFMA; 4 rows
@@ -806,8 +806,13 @@ hipError_t linear_quant(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t
             done = left < kMaxGroups * 16 ? left : kMaxGroups * 16;
             status = launch_mma<kQ8>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else if (left == 2) {
+            // Two rows: Q4_0 splits the chunks over the block's 4 waves as
+            // one row does (106 VGPRs, 4 waves per SIMD: [28672, 8192]
+            // 32.4-32.7 us against 33.2-33.4 unsplit); Q8_0 does not (130
+            // VGPRs leave 3 waves per SIMD: 48.5 against 45.5 us)
             done = 2;
-            status = launch_gemv<kQ8, 2, 4, false>(x + r0 * in, w, y + r0 * out, done, in, out, s);
+            status = kQ8 ? launch_gemv<kQ8, 2, 4, false>(x + r0 * in, w, y + r0 * out, done, in, out, s)
+                         : launch_gemv<kQ8, 2, 4, true>(x + r0 * in, w, y + r0 * out, done, in, out, s);
         } else {
             done = left < kMaxGroups ? left : kMaxGroups;
             status = launch_gemv<kQ8, 1, 4, true>(x + r0 * in, w, y + r0 * out, done, in, out, s);

@@ -305,6 +305,8 @@ QUANT_SHAPES = [  # rows, in, out
     # one row: a block's 4 waves split the 64-block chunks -- wave 1 with a
     # partial chunk; 6 chunks, so waves 0 and 1 take two (the second partial)
     (1, 2112, 5), (1, 10336, 9),
+    # two rows: Q4_0 splits the chunks the same way, Q8_0 does not
+    (2, 10336, 9), (2, 2112, 70),
     # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
