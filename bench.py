@@ -539,8 +539,8 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
             2 * tokens * width * 2 + tokens * 4, tokens * width)
     del emb_table
     # quantized linear (HBM-bound on the packed weights): a [28672, 8192]
-    # Q8_0 / Q4_0 matrix (a 70B-class MLP up+gate projection) times 1 or 4 f16
-    # rows (the GEMV) or 16 rows (the MFMA kernel: small-batch decode);
+    # Q8_0 / Q4_0 matrix (a 70B-class MLP up+gate projection) times 1 f16 row
+    # (the GEMV) or 4 and 16 rows (the MFMA kernel: small-batch decode);
     # synthetic packed bytes with an f16 scale of 2^-7
     rng = np.random.default_rng(7)
     def packed_weights(out, inw, block):
@@ -549,7 +549,7 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
         return raw
     for fmt, block in (("q8_0", 34), ("q4_0", 18)):
         out_f, in_f = 28672, 8192
-        row_counts = [r for r in ((1, 4, 16) if fmt == "q8_0" else (1,))
+        row_counts = [r for r in ((1, 4, 16) if fmt == "q8_0" else (1, 4))
                       if wanted(f"linear_{fmt}_f16_{r}x{in_f}_to_{out_f}")]
         if not row_counts:
             continue
@@ -882,6 +882,9 @@ def pmc_probe(sdk, reps=3):
     del packed
     ops.append(("linear_q4_0_f16_1x8192_to_28672",
                 lambda: sdk.call("tensor_linear_q4_0_f16", t["x8"], t["w4"], t["y4"])))
+    t["y44"] = T("f16", (4, 28672))
+    ops.append(("linear_q4_0_f16_4x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q4_0_f16", t["x84"], t["w4"], t["y44"])))
     t["wl"] = filled("f16", (8192, 8192), "normal", 7, 5, 0.0, 0.01)
     t["yl"] = T("f16", (1, 8192))
     ops.append(("linear_f16_1x8192_to_8192",

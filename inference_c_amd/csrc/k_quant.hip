@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
     }
 }
 
-// quant_mma_kernel (16 input rows per block row): each 32-weight block of 16
+// quant_mma_kernel (kXRows = 16 input rows per block row, or 4): each 32-weight block of 16
 // output rows o is one v_mfma_f32_16x16x32_f16 against the same block of 16
 // x rows r: B = the 16 x 32 weight tile, lane l holding o = l % 16 and 8 of
 // its k, decoded exactly to f16; A = the x rows at the same k; D[r][o] lands
@@ -408,9 +408,9 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 // nibbles of value bytes 4g .. 4g+3) and 16+4g .. 16+4g+3 (their high
 // nibbles), so a Q4 lane reads one 4-byte word per block.
 //
-// Data movement. A block's 4 waves own 4 tiles of 16 output rows and walk
-// the same weight blocks (k) in chunks of 16, so the x rows of a chunk (up
-// to 16 rows x 1 KB) are loaded once per block -- contiguous 16-byte loads
+// Data movement. A block's kWaves = 4 waves own 4 tiles of 16 output rows
+// and walk the same weight blocks (k) in chunks of 16, so the x rows of a
+// chunk (up to 16 rows x 1 KB) are loaded once per block -- contiguous 16-byte loads
 // into a double-buffered LDS chunk -- and every wave reads its MFMA operand
 // from there. (Each wave loading x in the MFMA layout itself moved 1 KB per
 // 512 weights through the address unit and bound the kernel.) Each wave
@@ -420,15 +420,17 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 // and barriers alone take 44-50 us, the decode and MFMAs alone ~40 us
 // (about 2 waves per SIMD: 448 blocks, and a k split per block does not fit
 // in LDS); prefetching 2 or 3 chunks ahead, or issuing the offset MFMA
-// first, measured no faster.
-template <bool kQ8>
-__global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__restrict__ x,
-                                                           const uint8_t *__restrict__ w,
-                                                           uint16_t *__restrict__ y,
-                                                           uint32_t rows, uint32_t in,
-                                                           uint32_t out) {
+// first, measured no faster. One-wave blocks (kWaves = 1, kXRows = 4: each
+// wave stages its own x) serve Q4_0 with up to 4 input rows.
+template <bool kQ8, uint32_t kWaves, uint32_t kXRows>
+__global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_t *__restrict__ x,
+                                                                   const uint8_t *__restrict__ w,
+                                                                   uint16_t *__restrict__ y,
+                                                                   uint32_t rows, uint32_t in,
+                                                                   uint32_t out) {
     constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
-    constexpr uint32_t kTiles = kBlock / kWave;               // output tiles per block
+    constexpr uint32_t kThreads = kWave * kWaves;
+    constexpr uint32_t kTiles = kWaves;                       // output tiles per block
     // weight blocks per chunk: a row's chunk is 544 (Q8) or 288 bytes
     // contiguous. 8 blocks ran ~45% slower (shorter runs per row at the
     // memory); 32 do not fit twice per CU in LDS.
@@ -441,10 +443,11 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
     constexpr uint32_t kStage = 16 * kRowStride;              // weight bytes per wave
     constexpr uint32_t kXSegs = kChunk * 4;                   // 16-byte segments of an x row's chunk
     constexpr uint32_t kXRow = kXSegs * 16 + 16;              // (+ bank pad)
-    constexpr uint32_t kXBuf = 16 * kXRow;
-    constexpr uint32_t kXPasses = 16 * kXSegs / kBlock;       // x segments per thread
+    constexpr uint32_t kXBuf = kXRows * kXRow;
+    constexpr uint32_t kXPasses = kXRows * kXSegs / kThreads; // x segments per thread
     static_assert(kChunkBytes % 16 == 0, "chunks start at one offset in their first segment");
-    static_assert(16 * kXSegs % kBlock == 0, "x chunks split evenly over the threads");
+    static_assert(kXRows * kXSegs % kThreads == 0, "x chunks split evenly over the threads");
+    static_assert(kXRows % 4 == 0 && kXRows <= 16, "whole row groups of the MFMA's D");
     __shared__ __attribute__((aligned(16))) uint8_t wstage[kTiles * kStage];
     __shared__ __attribute__((aligned(16))) uint8_t xstage[2][kXBuf];
     const uint32_t lane = threadIdx.x & (kWave - 1);
@@ -456,8 +459,8 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
     const uint32_t o0 = blockIdx.x * (16 * kTiles) + 16 * tile_i;
     const uint32_t t0 = min(o0, out - 1);
     const uint32_t last_row = min(15u, out - 1 - t0);
-    const uint32_t r0 = blockIdx.y * 16;
-    const uint32_t xrows = min(16u, rows - r0);
+    const uint32_t r0 = blockIdx.y * kXRows;
+    const uint32_t xrows = min(kXRows, rows - r0);
     const uint32_t blocks = in / 32;
     const uint64_t row_bytes = (uint64_t)blocks * kBytes;
     const uint32_t col = lane % 16, grp = lane / 16;
@@ -522,7 +525,7 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
         const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
 #pragma unroll
         for (int i = 0; i < (int)kXPasses; ++i) {
-            const uint32_t flat = pt + kBlock * i, xr = flat / kXSegs;
+            const uint32_t flat = pt + kThreads * i, xr = flat / kXSegs;
             const uint32_t sg = min(flat % kXSegs, nb * 4 - 1);
             if (xr < xrows)
                 xseg[i] = *reinterpret_cast<const u32x4 *>(x_tile + (uint64_t)xr * in +
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
             if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
 #pragma unroll
         for (int i = 0; i < (int)kXPasses; ++i) {
-            const uint32_t flat = pt + kBlock * i, xr = flat / kXSegs;
+            const uint32_t flat = pt + kThreads * i, xr = flat / kXSegs;
             if (xr < xrows) *reinterpret_cast<u32x4 *>(xbuf + xr * kXRow + (flat % kXSegs) * 16) = xseg[i];
         }
         // every wave's x rows and this wave's weights are in LDS; every wave
@@ -628,7 +631,7 @@ __global__ __launch_bounds__(kBlock) void quant_mma_kernel(const uint16_t *__res
 #pragma unroll 1
     for (int i = 0; i < 4; ++i) {
         const uint32_t r = r0 + 4 * grp + i;
-        if (r >= rows || o >= out) continue;
+        if (4 * grp + i >= kXRows || r >= rows || o >= out) continue;
         float v = acc[0];
         v = i == 1 ? acc[1] : v;
         v = i == 2 ? acc[2] : v;
@@ -762,10 +765,22 @@ hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t 
 template <bool kQ8>
 hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows, size_t in,
                       size_t out, hipStream_t s) {
+    if (!kQ8 && rows <= 4) {
+        // Q4_0, up to 4 rows: one wave per block staging its own x rows, so
+        // the tiles spread evenly over the CUs and no wave waits on another
+        // ([28672, 8192], two boxes: 3 rows 31.8-33.5 us against 36.2-37.3
+        // for 4-wave blocks, 4 rows 33.3-37.2 against 36.7-37.6). Q8_0 runs
+        // slower that way (4 rows 50.5 against 47.2-47.8 us): its per-wave
+        // rate, not the spread, bounds it.
+        const dim3 grid((unsigned)((out + 15) / 16), 1);
+        quant_mma_kernel<kQ8, 1, 4><<<grid, kWave, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                          (uint32_t)out);
+        return hipGetLastError();
+    }
     constexpr size_t kRowsPerBlock = 16 * (kBlock / kWave);
     const dim3 grid((unsigned)((out + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)((rows + 15) / 16));
-    quant_mma_kernel<kQ8><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                  (uint32_t)out);
+    quant_mma_kernel<kQ8, kBlock / kWave, 16><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
+                                                                      (uint32_t)out);
     return hipGetLastError();
 }
 

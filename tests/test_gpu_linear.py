@@ -310,6 +310,9 @@ QUANT_SHAPES = [  # rows, in, out
     # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
+    # the MFMA kernel at in a multiple of 2048 (4, 8 and 12 chunks per row);
+    # Q4_0 with 3 rows takes one-wave blocks
+    (3, 2048, 17), (16, 4096, 70), (20, 6144, 130),
     # drawn once with numpy's default_rng(5): rows 1-40, in up to 16384
     (16, 13216, 68), (17, 7712, 1546), (8, 4704, 2938), (1, 4576, 1150), (8, 6720, 394),
     (1, 16384, 573), (3, 7136, 790), (40, 2912, 2693), (4, 10304, 1479), (1, 15744, 1667),
@@ -370,6 +373,36 @@ def test_quantized_linear_non_finite(sdk, orc, fmt, shape):
         xf = x[finite]
         check(got[finite].astype(np.float16), want[finite].astype(np.float16),
               orc.linear_quant_abs_weight(xf, packed, fmt == 1), "f16", f"{name} {shape} finite rows")
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("rows", [3, 5])
+def test_quantized_linear_weight_offsets(sdk, orc, fmt, rows):
+    """The MFMA kernel (4-wave blocks; one-wave blocks for Q4_0 with 3 rows)
+    with the packed weights at byte offsets 4 .. 124 from a 256-byte
+    boundary: every offset moves the chunks within their 16-byte segments
+    and 128-byte lines. The decode and the sums do not depend on the offset,
+    so every result equals the aligned one bit for bit."""
+    inw, out = 2048, 37
+    x = orc.normal((rows, inw), 70, 0, 0.0, 1.0, "f16")
+    packed = orc.quantize(orc.normal((out, inw), 70, 1, 0.0, 1.0, "f16"), fmt)
+    want = orc.linear_quant(x, packed, fmt == 1)
+    weight = orc.linear_quant_abs_weight(x, packed, fmt == 1)
+    tag = "q8_0" if fmt == 1 else "q4_0"
+    dev = slot(sdk, f"linear_{tag}_f16_device", P, P, P, Z, Z, Z)
+    tx = sdk.from_numpy(x)
+    ty = sdk.tensor("f16", (rows, out))
+    aligned = None
+    for off in (0, 4, 12, 16, 64, 100, 124):
+        tw = sdk.from_numpy(np.concatenate([np.zeros(off, np.uint8), packed.ravel()]), dtype="u8")
+        assert tw.device_ptr() % 256 == 0
+        assert dev(tx.device_ptr(), tw.device_ptr() + off, ty.device_ptr(), rows, inw, out)
+        got = ty.download()
+        if aligned is None:
+            check(got, want, weight, "f16", f"{tag} weights at offset 0")
+            aligned = got
+        else:
+            assert_bits_equal(got, aligned, f"{tag} weights at offset {off}")
 
 
 def test_quantized_linear_reference_check(sdk, orc):
