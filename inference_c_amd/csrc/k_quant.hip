@@ -422,7 +422,7 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 // in LDS); prefetching 2 or 3 chunks ahead, or issuing the offset MFMA
 // first, measured no faster. One-wave blocks (kWaves = 1, kXRows = 4: each
 // wave stages its own x) serve Q4_0 with up to 4 input rows.
-template <bool kQ8, uint32_t kWaves, uint32_t kXRows>
+template <bool kQ8, uint32_t kWaves, uint32_t kXRows, uint32_t kChunk>
 __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_t *__restrict__ x,
                                                                    const uint8_t *__restrict__ w,
                                                                    uint16_t *__restrict__ y,
@@ -433,8 +433,10 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     constexpr uint32_t kTiles = kWaves;                       // output tiles per block
     // weight blocks per chunk: a row's chunk is 544 (Q8) or 288 bytes
     // contiguous. 8 blocks ran ~45% slower (shorter runs per row at the
-    // memory); 32 do not fit twice per CU in LDS.
-    constexpr uint32_t kChunk = 16;
+    // memory); 32 do not fit twice per CU in LDS with 4-wave blocks. The
+    // one-wave blocks (Q4_0, up to 4 rows) take 32: half the chunk
+    // boundaries, whose 128-byte lines are read twice (4 rows: 1.20 -> 1.07
+    // x the packed bytes, the same time).
     constexpr uint32_t kChunkBytes = kChunk * kBytes;         // a multiple of 16
     constexpr uint32_t kVecs = kChunkBytes / 16 + 2;          // segments covering a row's chunk
     constexpr uint32_t kRowStride = (kVecs + 1) * 16;         // one spare segment per row: banks
@@ -449,7 +451,10 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     static_assert(kXRows * kXSegs % kThreads == 0, "x chunks split evenly over the threads");
     static_assert(kXRows % 4 == 0 && kXRows <= 16, "whole row groups of the MFMA's D");
     __shared__ __attribute__((aligned(16))) uint8_t wstage[kTiles * kStage];
-    __shared__ __attribute__((aligned(16))) uint8_t xstage[2][kXBuf];
+    // x double-buffered when waves share it; a lone wave reuses one buffer
+    // (its reads of a chunk come before its stores of the next)
+    constexpr uint32_t kXBufs = kWaves > 1 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[kXBufs][kXBuf];
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t tile_i = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t pt = threadIdx.x;
@@ -558,7 +563,7 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     for (uint32_t step = 0; step < steps; ++step) {
         const uint32_t c0 = kb0 + step * kChunk;
         const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
-        uint8_t *xbuf = xstage[step & 1u];
+        uint8_t *xbuf = xstage[step % kXBufs];
 #pragma unroll
         for (int i = 0; i < (int)kPasses; ++i)
             if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
@@ -765,22 +770,24 @@ hipError_t launch_gemv(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t 
 template <bool kQ8>
 hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t rows, size_t in,
                       size_t out, hipStream_t s) {
-    if (!kQ8 && rows <= 4) {
-        // Q4_0, up to 4 rows: one wave per block staging its own x rows, so
-        // the tiles spread evenly over the CUs and no wave waits on another
-        // ([28672, 8192], two boxes: 3 rows 31.8-33.5 us against 36.2-37.3
-        // for 4-wave blocks, 4 rows 33.3-37.2 against 36.7-37.6). Q8_0 runs
-        // slower that way (4 rows 50.5 against 47.2-47.8 us): its per-wave
-        // rate, not the spread, bounds it.
-        const dim3 grid((unsigned)((out + 15) / 16), 1);
-        quant_mma_kernel<kQ8, 1, 4><<<grid, kWave, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                          (uint32_t)out);
-        return hipGetLastError();
+    if constexpr (!kQ8) {
+        if (rows <= 4) {
+            // Q4_0, up to 4 rows: one wave per block staging its own x rows,
+            // so the tiles spread evenly over the CUs and no wave waits on
+            // another ([28672, 8192], two boxes: 3 rows 31.8-33.5 us against
+            // 36.2-37.3 for 4-wave blocks, 4 rows 33.3-37.2 against
+            // 36.7-37.6). Q8_0 runs slower that way (4 rows 50.5 against
+            // 47.2-47.8 us): its per-wave rate, not the spread, bounds it.
+            const dim3 grid((unsigned)((out + 15) / 16), 1);
+            quant_mma_kernel<kQ8, 1, 4, 32><<<grid, kWave, 0, s>>>(x, w, y, (uint32_t)rows,
+                                                                  (uint32_t)in, (uint32_t)out);
+            return hipGetLastError();
+        }
     }
     constexpr size_t kRowsPerBlock = 16 * (kBlock / kWave);
     const dim3 grid((unsigned)((out + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)((rows + 15) / 16));
-    quant_mma_kernel<kQ8, kBlock / kWave, 16><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows, (uint32_t)in,
-                                                                      (uint32_t)out);
+    quant_mma_kernel<kQ8, kBlock / kWave, 16, 16><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows,
+                                                                          (uint32_t)in, (uint32_t)out);
     return hipGetLastError();
 }
 
