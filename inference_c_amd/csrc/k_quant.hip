@@ -431,8 +431,8 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     constexpr uint32_t kBytes = Fmt<kQ8>::kBytes;
     constexpr uint32_t kThreads = kWave * kWaves;
     constexpr uint32_t kTiles = kWaves;                       // output tiles per block
-    // weight blocks per chunk: a row's chunk is 544 (Q8) or 288 bytes
-    // contiguous. 8 blocks ran ~45% slower (shorter runs per row at the
+    // kChunk weight blocks per chunk; at 16 a row's chunk is 544 (Q8) or
+    // 288 bytes contiguous. 8 blocks ran ~45% slower (shorter runs per row at the
     // memory); 32 do not fit twice per CU in LDS with 4-wave blocks. The
     // one-wave blocks (Q4_0, up to 4 rows) take 32: half the chunk
     // boundaries, whose 128-byte lines are read twice (4 rows: 1.20 -> 1.07
