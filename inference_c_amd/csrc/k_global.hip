@@ -3,7 +3,10 @@
 // Two passes. Pass 1 (sum+max): block b streams the contiguous chunk of
 // kChunk 16-byte vectors starting at b * kChunk, kVpl vectors in flight per
 // lane per step (one-shot chunks measured ~15% faster on MI355X than a
-// persistent grid-stride loop: 88% vs 76% of HBM peak reading 4 GiB); past
+// persistent grid-stride loop: 88% vs 76% of HBM peak reading 4 GiB; 32
+// vectors x 4 steps per lane, 150 VGPRs and 3 waves per SIMD, ran 2^30 f32
+// in 607.9-608.9 us against 612.1-613.5 for 8 x 16 at 8 waves per SIMD,
+// and 16 x 8 or 16 x 16 in between); past
 // kMaxPartials chunks the grid strides over chunks. Each lane folds every
 // step's 32 values in f32 and adds the step total to an f64 accumulator, so
 // the rounding error stays near 32 f32 ulps of the step magnitude regardless
@@ -21,8 +24,8 @@ namespace {
 
 constexpr int kPartials = 2048;     // argmax pass-1 grid
 constexpr int kUnroll = 4;          // argmax vectors in flight per lane
-constexpr int kVpl = 8;             // sum+max vectors in flight per lane
-constexpr int kSteps = 16;          // sum+max steps per chunk
+constexpr int kVpl = 32;            // sum+max vectors in flight per lane
+constexpr int kSteps = 4;           // sum+max steps per chunk
 constexpr size_t kChunk = (size_t)kBlock * kVpl * kSteps;  // 512 KiB of f32
 constexpr int kMaxPartials = 8192;  // sum+max pass-1 grid cap (4 GiB per sweep)
 constexpr int kFoldBlock = 1024;    // pass-2 lanes
