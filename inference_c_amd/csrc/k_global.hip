@@ -3,13 +3,13 @@
 // Two passes. Pass 1 (sum+max): block b streams the contiguous chunk of
 // kChunk 16-byte vectors starting at b * kChunk, kVpl vectors in flight per
 // lane per step (one-shot chunks measured ~15% faster on MI355X than a
-// persistent grid-stride loop: 88% vs 76% of HBM peak reading 4 GiB; 32
-// vectors x 4 steps per lane, 150 VGPRs and 3 waves per SIMD, ran 2^30 f32
-// in 607.9-608.9 us against 612.1-613.5 for 8 x 16 at 8 waves per SIMD,
-// and 16 x 8 or 16 x 16 in between); past
+// persistent grid-stride loop: 88% vs 76% of HBM peak reading 4 GiB). 32
+// vectors x 8 steps per lane (1 MiB chunks, 150 VGPRs, 3 waves per SIMD)
+// ran 2^30 f32 in 606.2-606.8 us, 32 x 4 in 607.7-609.7 and 8 x 16 (8 waves
+// per SIMD) in 612.1-613.5; 32 x 16 and 32 x 32 slower again. Past
 // kMaxPartials chunks the grid strides over chunks. Each lane folds every
-// step's 32 values in f32 and adds the step total to an f64 accumulator, so
-// the rounding error stays near 32 f32 ulps of the step magnitude regardless
+// 32 values (8 vectors) in f32 and adds that total to an f64 accumulator, so
+// the rounding error stays near 32 f32 ulps of the group magnitude regardless
 // of the tensor size. Lanes combine through shuffles, waves through LDS, and
 // each block writes one partial. Pass 2: one 1024-lane block loads all
 // partials at once, folds them in f64 and writes the result. No atomics and
@@ -24,10 +24,11 @@ namespace {
 
 constexpr int kPartials = 2048;     // argmax pass-1 grid
 constexpr int kUnroll = 4;          // argmax vectors in flight per lane
-constexpr int kVpl = 32;            // sum+max vectors in flight per lane
-constexpr int kSteps = 4;           // sum+max steps per chunk
-constexpr size_t kChunk = (size_t)kBlock * kVpl * kSteps;  // 512 KiB of f32
-constexpr int kMaxPartials = 8192;  // sum+max pass-1 grid cap (4 GiB per sweep)
+constexpr int kVpl = 32;            // sum+max vectors in flight per lane (a multiple of 8)
+constexpr int kSteps = 8;           // sum+max steps per chunk
+constexpr size_t kChunk = (size_t)kBlock * kVpl * kSteps;  // 1 MiB of f32
+static_assert(kVpl % 8 == 0, "whole f32 groups of 8 vectors");
+constexpr int kMaxPartials = 8192;  // sum+max pass-1 grid cap (8 GiB per sweep)
 constexpr int kFoldBlock = 1024;    // pass-2 lanes
 
 struct Partial {
@@ -63,15 +64,19 @@ __device__ inline void sum_max_chunk(const f32x4 *__restrict__ xv, size_t first,
                 v[u] = __builtin_nontemporal_load(xv + i);
             }
         }
-        float group = 0.0f;
+        // groups of 8 vectors (32 values) fold in f32, each into the f64 total
 #pragma unroll
-        for (int u = 0; u < kVpl; ++u) {
-            if constexpr (kGuard) {
-                if (base + (size_t)u * kBlock >= nvec) continue;
+        for (int g = 0; g < kVpl / 8; ++g) {
+            float group = 0.0f;
+#pragma unroll
+            for (int u = 8 * g; u < 8 * g + 8; ++u) {
+                if constexpr (kGuard) {
+                    if (base + (size_t)u * kBlock >= nvec) continue;
+                }
+                fold(v[u], group, m, nan);
             }
-            fold(v[u], group, m, nan);
+            total += (double)group;
         }
-        total += (double)group;
     }
 }
 
