@@ -169,7 +169,7 @@ int tensor_sum_max_f32(const TensorBuffer *input, TensorBuffer *sum_output,
    under HIP graph capture, serving loops that forbid hipMalloc). Same
    validation, kernels and results as tensor_sum_max_f32; every operand must
    be a device tensor (host operands are refused, since staging them would
-   allocate). The pass-1 partials live in a 128 KiB device array of the
+   allocate). The pass-1 partials live in a 64 KiB device array of the
    library, one per GPU, held until the process ends; it covers every input
    size (the pass-1 grid is capped), and a launch whose partials would not fit
    is refused with a message. Pass 1 writes every partial pass 2 reads, so

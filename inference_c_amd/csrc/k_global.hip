@@ -28,7 +28,7 @@ constexpr int kVpl = 32;            // sum+max vectors in flight per lane (a mul
 constexpr int kSteps = 8;           // sum+max steps per chunk
 constexpr size_t kChunk = (size_t)kBlock * kVpl * kSteps;  // 1 MiB of f32
 static_assert(kVpl % 8 == 0, "whole f32 groups of 8 vectors");
-constexpr int kMaxPartials = 8192;  // sum+max pass-1 grid cap (8 GiB per sweep)
+constexpr int kMaxPartials = 4096;  // sum+max pass-1 grid cap (4 GiB per sweep: 2^30 f32 one-shot)
 constexpr int kFoldBlock = 1024;    // pass-2 lanes
 
 struct Partial {
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kBlock) void sum_max_pass1(const float *__restrict_
     }
 }
 
-// count <= kMaxPartials = 8 * kFoldBlock: every lane's partials are
+// count <= kMaxPartials = 4 * kFoldBlock: every lane's partials are
 // requested before any is folded.
 __global__ __launch_bounds__(kFoldBlock) void sum_max_pass2(const Partial *__restrict__ partials,
                                                             int count, double *sum_out,
@@ -266,7 +266,7 @@ inline int pass1_grid(size_t work) {
 
 // Partials of the allocation-free sum+max (tensor_sum_max_f32_no_alloc): one
 // Partial per pass-1 block, and the pass-1 grid never exceeds kMaxPartials
-// blocks (past that the blocks stride over chunks), so 128 KiB covers every
+// blocks (past that the blocks stride over chunks), so 64 KiB covers every
 // input size. Each device the library runs on holds its own copy until the
 // process ends. Host code never passes this name to a kernel: its device
 // address comes from hipGetSymbolAddress, once per device.

@@ -57,9 +57,10 @@ def test_sum_max_two_pow_30(sdk, orc):
 
 
 def test_sum_max_past_one_sweep(sdk, orc):
-    """More than 8192 chunks of 2^17 floats: pass-1 blocks stride over a
-    second sweep of chunks, ending in a partial chunk and a ragged tail."""
-    n = 8192 * (1 << 17) + 3 * (1 << 17) + 1000 * 4 + 3
+    """More than 4096 chunks of 2^18 floats (one sweep of the capped pass-1
+    grid): pass-1 blocks stride over a second sweep of chunks, ending in a
+    partial chunk and a ragged tail."""
+    n = 4096 * (1 << 18) + 3 * (1 << 17) + 1000 * 4 + 3
     t = sdk.tensor("f32", (n,))
     sdk.call("tensor_fill_uniform", t, 0, 7, -1.0, 1.0)
     ts, tm = sdk.tensor("f64", (1,)), sdk.tensor("f32", (1,))
@@ -69,7 +70,7 @@ def test_sum_max_past_one_sweep(sdk, orc):
     assert abs(float(ts.download()[0]) - want_s) <= 1e-6 * abs_s
     assert tm.download()[0] == want_m
     x[n - 2] = 7.5  # in the ragged tail
-    x[8192 * (1 << 17) + 17] = 3.0  # in the second sweep
+    x[4096 * (1 << 18) + 17] = 3.0  # in the second sweep
     s, m = sum_max(sdk, x)
     assert m == 7.5 and abs(s - orc.sum_max(x)[0]) <= 1e-6 * abs_s
 
