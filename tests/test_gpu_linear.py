@@ -310,8 +310,8 @@ QUANT_SHAPES = [  # rows, in, out
     # the MFMA kernel (2+ rows): one weight block and one output; 16 rows over
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
-    # the MFMA kernel at in a multiple of 2048 (4, 8 and 12 chunks per row);
-    # Q4_0 with 3 rows takes one-wave blocks
+    # the MFMA kernel at in a multiple of 2048 (4, 8 and 12 16-block chunks
+    # per row); Q4_0 with 3 rows takes one-wave blocks of 32-block chunks
     (3, 2048, 17), (16, 4096, 70), (20, 6144, 130),
     # drawn once with numpy's default_rng(5): rows 1-40, in up to 16384
     (16, 13216, 68), (17, 7712, 1546), (8, 4704, 2938), (1, 4576, 1150), (8, 6720, 394),
