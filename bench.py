@@ -645,6 +645,17 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
         return filled("f32", (1 << 30,), "uniform", 0, 0, -1.0, 1.0), T("f64", (1,)), T("f32", (1,))
     measure("cfg5_global_sum_max_f32", cfg5_global,
             lambda s: sdk.call("tensor_sum_max_f32", s[0], s[1], s[2]), 4_294_967_296, 1_073_741_824)
+    # argmax, the scan of the same row: 2^28 f16 N(0,1) (512 MiB, HBM-bound)
+    # and one decode step's logits over a 128 256-entry f32 vocabulary
+    # (greedy sampling; launch-bound)
+    def argmax_big():
+        return filled("f16", (1 << 28,), "normal", 0, 3, 0.0, 1.0), T("u32", (1,))
+    measure("argmax_f16_2p28", argmax_big, lambda s: sdk.call("tensor_argmax_f16", s[0], s[1]),
+            (1 << 28) * 2 + 4, 1 << 28)
+    def argmax_vocab():
+        return filled("f32", (128256,), "normal", 0, 4, 0.0, 1.0), T("u32", (1,))
+    measure("argmax_f32_vocab_128256", argmax_vocab,
+            lambda s: sdk.call("tensor_argmax_f32", s[0], s[1]), 128256 * 4 + 4, 128256)
     return results
 
 
