@@ -1,6 +1,8 @@
 """Pins the oracle's f16/bf16 conversions (and the library's host scalar
 conversions) against the reference build, exhaustively, and against the
 reference's own known answers (tests/test_tensor_buffer.c:19-67)."""
+import ctypes
+import math
 import os
 import subprocess
 
@@ -35,6 +37,27 @@ def test_oracle_conversions_exhaustive_vs_reference():
 def test_library_host_conversions_vs_reference():
     """include/tensor_f16.h of the HIP library: every f16, every 3rd f32."""
     _run_checker(PRODUCT_LIB, "tensor_f32_to_f16", "tensor_f16_to_f32", 3)
+
+
+def test_library_bf16_widening_vs_reference():
+    """include/tensor_f16.h tensor_bf16_to_f32 of the HIP library against the
+    reference build's (src/common/tensor_f16.c): all 65536 bf16 patterns, the
+    same value and sign (NaNs: both NaN). A host function: no GPU needed."""
+    if not os.path.exists(REF_LIB):
+        pytest.skip("reference build absent")
+    ref, lib = ctypes.CDLL(REF_LIB), ctypes.CDLL(PRODUCT_LIB)
+    for f in (ref.tensor_bf16_to_f32, lib.tensor_bf16_to_f32):
+        f.argtypes, f.restype = [ctypes.c_uint16], ctypes.c_float
+    bad = 0
+    for bits in range(65536):
+        a, b = ref.tensor_bf16_to_f32(bits), lib.tensor_bf16_to_f32(bits)
+        if math.isnan(a) or math.isnan(b):
+            bad += not (math.isnan(a) and math.isnan(b))
+        else:
+            bad += not (a == b and math.copysign(1.0, a) == math.copysign(1.0, b))
+    assert bad == 0
+    # exact widening: the pattern is the high half of the f32
+    assert lib.tensor_bf16_to_f32(0x3F80) == 1.0 and lib.tensor_bf16_to_f32(0xC000) == -2.0
 
 
 def test_reference_known_answers(orc):
