@@ -421,8 +421,10 @@ __global__ __launch_bounds__(kBlock) void quant_gemv_kernel(const uint16_t *__re
 // (about 2 waves per SIMD: 448 blocks, and a k split per block does not fit
 // in LDS); prefetching 2 or 3 chunks ahead, or issuing the offset MFMA
 // first, measured no faster. One-wave blocks (kWaves = 1, kXRows = 4: each
-// wave stages its own x) serve Q4_0 with up to 4 input rows.
-template <bool kQ8, uint32_t kWaves, uint32_t kXRows, uint32_t kChunk>
+// wave stages its own x) serve Q4_0 with up to 4 input rows. kLines (Q8_0
+// with rows at one phase to the 128-byte lines) loads each line of the
+// weights once, carrying a chunk's first bytes over from the chunk before.
+template <bool kQ8, uint32_t kWaves, uint32_t kXRows, uint32_t kChunk, bool kLines>
 __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_t *__restrict__ x,
                                                                    const uint8_t *__restrict__ w,
                                                                    uint16_t *__restrict__ y,
@@ -438,7 +440,13 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     // boundaries, whose 128-byte lines are read twice (4 rows: 1.20 -> 1.07
     // x the packed bytes, the same time).
     constexpr uint32_t kChunkBytes = kChunk * kBytes;         // a multiple of 16
-    constexpr uint32_t kVecs = kChunkBytes / 16 + 2;          // segments covering a row's chunk
+    // kLines: most bytes a chunk takes over from the chunk before, and a
+    // row's LDS window
+    constexpr uint32_t kCarry = kLines ? 96 : 0;
+    constexpr uint32_t kSpan = kChunkBytes + kCarry;
+    // segments a row's chunk is loaded from (kLines: its window; else the
+    // segments covering the chunk, one spare either side)
+    constexpr uint32_t kVecs = kLines ? kSpan / 16 : kChunkBytes / 16 + 2;
     constexpr uint32_t kRowStride = (kVecs + 1) * 16;         // one spare segment per row: banks
     constexpr uint32_t kSegs = 16 * kVecs;
     constexpr uint32_t kPasses = (kSegs + kWave - 1) / kWave;
@@ -448,6 +456,8 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
     constexpr uint32_t kXBuf = kXRows * kXRow;
     constexpr uint32_t kXPasses = kXRows * kXSegs / kThreads; // x segments per thread
     static_assert(kChunkBytes % 16 == 0, "chunks start at one offset in their first segment");
+    static_assert(!kLines || (kChunkBytes % 128 == 32 && kSegs % kWave == 0 && kWaves > 1),
+                  "line windows: chunks 32 bytes past a line multiple, whole passes, shared x");
     static_assert(kXRows * kXSegs % kThreads == 0, "x chunks split evenly over the threads");
     static_assert(kXRows % 4 == 0 && kXRows <= 16, "whole row groups of the MFMA's D");
     __shared__ __attribute__((aligned(16))) uint8_t wstage[kTiles * kStage];
@@ -484,11 +494,11 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
         return (uint32_t)((reinterpret_cast<uintptr_t>(tile) + (uint64_t)row * row_bytes) & 15u);
     };
     // the offset of segment v of a chunk of nb blocks, clamped onto the
-    // chunk's last segment
+    // chunk's last segment (kLines: not clamped; the line windows bound it)
     auto seg_off = [&](uint32_t v, uint32_t nb) -> uint32_t {
         const uint32_t row = min(min(v / kVecs, 15u), last_row), sidx = v % kVecs;
         const uint32_t lead = lead_of(row);
-        const uint32_t last = (lead + nb * kBytes + 15) / 16 - 1;
+        const uint32_t last = kLines ? kVecs - 1 : (lead + nb * kBytes + 15) / 16 - 1;
         return (uint32_t)(row * row_bytes) - lead + 16 + 16 * min(sidx, last);
     };
     uint32_t off_full[kPasses], lds_dst[kPasses];
@@ -498,17 +508,50 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
         off_full[i] = seg_off(v, kChunk);
         lds_dst[i] = min(v / kVecs, 15u) * kRowStride + (v % kVecs) * 16;
     }
+    // kLines (every row at one phase to the 128-byte lines: row_bytes a
+    // multiple of 128): each line is loaded by one chunk only. Chunk c loads
+    // the segments from where chunk c - 1 stopped to the end of the line
+    // holding its own last byte (at most F + kSpan, F = the chunk's start
+    // rounded down to 16; the row's last chunk stops at its last segment);
+    // the bytes [F, that start) -- at most kCarry, chunk c - 1 loaded them --
+    // move within each LDS row from kChunkBytes to 0. With g = F mod 128
+    // (one for all rows, repeating every 4 chunks) the window is
+    // [min(roundup128(g + lead) - g, kCarry) (0 for the first chunk),
+    //  min(roundup128(g + lead + kChunkBytes) - g, kSpan)) bytes past F, the
+    // last chunk's end ceil16(lead + nb * kBytes); packed ws | we << 16.
+    const uint32_t lead_u = lead_of(0);
+    const uint32_t g_base = (uint32_t)((reinterpret_cast<uintptr_t>(tile) - lead_u) & 127u);
+    const uint32_t last_c = steps - 1;
+    auto window = [&](uint32_t c) -> uint32_t {
+        const uint32_t g = (g_base + (c & 3u) * kChunkBytes) & 127u;
+        const uint32_t ws = c == 0 ? 0u : min(((g + lead_u + 127u) & ~127u) - g, kCarry);
+        const uint32_t we = c == last_c ? (lead_u + (kb1 - kChunk * c) * kBytes + 15u) & ~15u
+                                        : min(((g + lead_u + kChunkBytes + 127u) & ~127u) - g, kSpan);
+        return ws | max(we, ws) << 16;
+    };
+    auto in_window = [&](int i, uint32_t win) -> bool {
+        const uint32_t ws = win & 0xffffu, we = win >> 16;
+        return 16u * ((lane + kWave * (uint32_t)i) % kVecs) - ws < we - ws;
+    };
     u32x4 seg[kPasses];
     auto fetch_w = [&](uint32_t c0) {
         const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
         const uint8_t *base = tile + (uint64_t)c0 * kBytes - 16;
-        // Non-temporal loads. A row's 544-byte chunks are not line-aligned,
-        // so the line holding a chunk boundary is read by two consecutive
-        // chunks and, not kept in L2 in between, comes from HBM twice (1.13 x
-        // the packed bytes at 4 rows). L2-allocating loads read it once, but
-        // after other traffic has left the last-level cache dirty (a 600 MB
-        // write just before) the launch took 95 us instead of 48: the
-        // weights then evict that data. Back to back they gained nothing.
+        if constexpr (kLines) {
+            const uint32_t win = window(c0 / kChunk);
+#pragma unroll
+            for (int i = 0; i < (int)kPasses; ++i)
+                if (in_window(i, win))
+                    seg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off_full[i]));
+            return;
+        }
+        // Non-temporal loads. Without kLines a row's chunks are not
+        // line-aligned, so the line holding a chunk boundary is read by two
+        // consecutive chunks and, not kept in L2 in between, comes from HBM
+        // twice (Q8_0: 1.13 x the packed bytes at 4 rows). L2-allocating loads
+        // read it once, but after other traffic has left the last-level cache
+        // dirty (a 600 MB write just before) the launch took 95 us instead of
+        // 48: the weights then evict that data.
         if (nb == kChunk) {
 #pragma unroll
             for (int i = 0; i < (int)kPasses; ++i)
@@ -564,9 +607,37 @@ __global__ __launch_bounds__(kWave * kWaves) void quant_mma_kernel(const uint16_
         const uint32_t c0 = kb0 + step * kChunk;
         const uint32_t nb = min((uint32_t)kChunk, kb1 - c0);
         uint8_t *xbuf = xstage[step % kXBufs];
+        if constexpr (kLines) {
+            if (step > 0) {
+                // the bytes chunk c - 1 loaded for this chunk: kCarry bytes
+                // of each row move from kChunkBytes to 0 (what lies past the
+                // carried part is overwritten next)
+                constexpr uint32_t kMoves = kCarry / 16;
+                u32x4 moved[2];
 #pragma unroll
-        for (int i = 0; i < (int)kPasses; ++i)
-            if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
+                for (uint32_t m = 0; m < 2; ++m) {
+                    const uint32_t u = lane + kWave * m;
+                    if (u < 16 * kMoves)
+                        moved[m] = *reinterpret_cast<const u32x4 *>(region + (u / kMoves) * kRowStride +
+                                                                    kChunkBytes + (u % kMoves) * 16);
+                }
+#pragma unroll
+                for (uint32_t m = 0; m < 2; ++m) {
+                    const uint32_t u = lane + kWave * m;
+                    if (u < 16 * kMoves)
+                        *reinterpret_cast<u32x4 *>(region + (u / kMoves) * kRowStride + (u % kMoves) * 16) =
+                            moved[m];
+                }
+            }
+            const uint32_t win = window(step);
+#pragma unroll
+            for (int i = 0; i < (int)kPasses; ++i)
+                if (in_window(i, win)) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < (int)kPasses; ++i)
+                if (lane + kWave * i < kSegs) *reinterpret_cast<u32x4 *>(region + lds_dst[i]) = seg[i];
+        }
 #pragma unroll
         for (int i = 0; i < (int)kXPasses; ++i) {
             const uint32_t flat = pt + kThreads * i, xr = flat / kXSegs;
@@ -845,15 +916,29 @@ hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t r
             // 36.7-37.6). Q8_0 runs slower that way (4 rows 50.5 against
             // 47.2-47.8 us): its per-wave rate, not the spread, bounds it.
             const dim3 grid((unsigned)((out + 15) / 16), 1);
-            quant_mma_kernel<kQ8, 1, 4, 32><<<grid, kWave, 0, s>>>(x, w, y, (uint32_t)rows,
+            quant_mma_kernel<kQ8, 1, 4, 32, false><<<grid, kWave, 0, s>>>(x, w, y, (uint32_t)rows,
                                                                   (uint32_t)in, (uint32_t)out);
             return hipGetLastError();
         }
     }
     constexpr size_t kRowsPerBlock = 16 * (kBlock / kWave);
     const dim3 grid((unsigned)((out + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)((rows + 15) / 16));
-    quant_mma_kernel<kQ8, kBlock / kWave, 16, 16><<<grid, kBlock, 0, s>>>(x, w, y, (uint32_t)rows,
-                                                                          (uint32_t)in, (uint32_t)out);
+    // Q8_0 from 7 rows, rows at one phase to the 128-byte lines (in a
+    // multiple of 2048): each line loaded once (1.002 x the packed bytes
+    // instead of 1.134 x). [28672, 8192] over three boxes: 7, 8 and 16 rows
+    // 1-3% faster that way, 3-6 rows 0.4-5% slower (the carry move and the
+    // masked extra load pass sit on each step's critical path), so fewer
+    // rows keep the per-chunk loads. Q4_0's 4-wave launches ran 12-14%
+    // slower that way (8 and 16 rows) and keep them too.
+    if constexpr (kQ8) {
+        if (rows >= 7 && in / 32 * Fmt<kQ8>::kBytes % 128 == 0) {
+            quant_mma_kernel<kQ8, kBlock / kWave, 16, 16, true><<<grid, kBlock, 0, s>>>(
+                x, w, y, (uint32_t)rows, (uint32_t)in, (uint32_t)out);
+            return hipGetLastError();
+        }
+    }
+    quant_mma_kernel<kQ8, kBlock / kWave, 16, 16, false><<<grid, kBlock, 0, s>>>(
+        x, w, y, (uint32_t)rows, (uint32_t)in, (uint32_t)out);
     return hipGetLastError();
 }
 

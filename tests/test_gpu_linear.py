@@ -311,8 +311,9 @@ QUANT_SHAPES = [  # rows, in, out
     # 8 full chunks and a 1-block chunk, ragged tiles; a 4-row second group
     (2, 32, 1), (16, 4128, 70), (20, 1056, 130),
     # the MFMA kernel at in a multiple of 2048 (4, 8 and 12 16-block chunks
-    # per row); Q4_0 with 3 rows takes one-wave blocks of 32-block chunks
-    (3, 2048, 17), (16, 4096, 70), (20, 6144, 130),
+    # per row; Q8_0 from 7 rows on line windows); Q4_0 with 3 rows takes
+    # one-wave blocks of 32-block chunks
+    (3, 2048, 17), (16, 4096, 70), (20, 6144, 130), (7, 2048, 33),
     # drawn once with numpy's default_rng(5): rows 1-40, in up to 16384
     (16, 13216, 68), (17, 7712, 1546), (8, 4704, 2938), (1, 4576, 1150), (8, 6720, 394),
     (1, 16384, 573), (3, 7136, 790), (40, 2912, 2693), (4, 10304, 1479), (1, 15744, 1667),
@@ -376,13 +377,15 @@ def test_quantized_linear_non_finite(sdk, orc, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("rows", [3, 5])
+@pytest.mark.parametrize("rows", [3, 5, 8])
 def test_quantized_linear_weight_offsets(sdk, orc, fmt, rows):
-    """The MFMA kernel (4-wave blocks; one-wave blocks for Q4_0 with 3 rows)
-    with the packed weights at byte offsets 4 .. 124 from a 256-byte
-    boundary: every offset moves the chunks within their 16-byte segments
-    and 128-byte lines. The decode and the sums do not depend on the offset,
-    so every result equals the aligned one bit for bit."""
+    """The MFMA kernel (4-wave blocks; one-wave blocks for Q4_0 with 3 rows;
+    for Q8_0 with 8 rows the line windows, each 128-byte line loaded once and
+    a chunk's first bytes carried over from the chunk before) with the
+    packed weights at byte offsets 4 .. 124 from a 256-byte boundary: every
+    offset moves the chunks within their 16-byte segments and 128-byte
+    lines. The decode and the sums do not depend on the offset, so every
+    result equals the aligned one bit for bit."""
     inw, out = 2048, 37
     x = orc.normal((rows, inw), 70, 0, 0.0, 1.0, "f16")
     packed = orc.quantize(orc.normal((out, inw), 70, 1, 0.0, 1.0, "f16"), fmt)
