@@ -886,6 +886,10 @@ def pmc_probe(sdk, reps=3):
     t["x84"], t["y84"] = filled("f16", (4, 8192), "normal", 7, 4, 0.0, 1.0), T("f16", (4, 28672))
     ops.append(("linear_q8_0_f16_4x8192_to_28672",
                 lambda: sdk.call("tensor_linear_q8_0_f16", t["x84"], t["w8"], t["y84"])))
+    # 16 rows: the MFMA kernel's line-window form (each 128-byte line once)
+    t["x816"], t["y816"] = filled("f16", (16, 8192), "normal", 7, 6, 0.0, 1.0), T("f16", (16, 28672))
+    ops.append(("linear_q8_0_f16_16x8192_to_28672",
+                lambda: sdk.call("tensor_linear_q8_0_f16", t["x816"], t["w8"], t["y816"])))
     packed = np.random.default_rng(8).integers(0, 256, size=(28672, 256, 18), dtype=np.uint8)
     packed[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -7).tobytes(), np.uint8)
     t["w4"] = T("u8", packed.shape).upload(packed)
