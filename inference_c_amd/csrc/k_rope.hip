@@ -339,6 +339,11 @@ __global__ __launch_bounds__(kBlock) void rope_group_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // -0 as an addend the compiler cannot fold: fma(a, b, -0) rounds a * b
+    // once, the same value as the product, so the f16 paths below multiply
+    // with v_fma_mix_f32 (the f16 operand widened inside the instruction)
+    float nz;
+    asm("v_mov_b32 %0, 0x80000000" : "=v"(nz));
     float ca[E], cb[E];   // this side's coefficients of the left and right values
 #pragma unroll
     for (int u = 0; u < kIt; ++u) {
@@ -366,10 +371,17 @@ __global__ __launch_bounds__(kBlock) void rope_group_kernel(
         const Vec16<S> lv = __builtin_bit_cast(Vec16<S>, uint4{lw[0], lw[1], lw[2], lw[3]});
         const Vec16<S> rv = __builtin_bit_cast(Vec16<S>, uint4{rw[0], rw[1], rw[2], rw[3]});
         Vec16<S> out;
+        if constexpr (std::is_same_v<S, _Float16>) {
 #pragma unroll
-        for (uint32_t e = 0; e < E; ++e)
-            out.v[e] = Elem<S>::store(Elem<S>::load(lv.v[e]) * ca[e] +
-                                      Elem<S>::load(rv.v[e]) * cb[e]);
+            for (uint32_t e = 0; e < E; ++e)
+                out.v[e] = (_Float16)(__builtin_fmaf((float)lv.v[e], ca[e], nz) +
+                                      __builtin_fmaf((float)rv.v[e], cb[e], nz));
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < E; ++e)
+                out.v[e] = Elem<S>::store(Elem<S>::load(lv.v[e]) * ca[e] +
+                                          Elem<S>::load(rv.v[e]) * cb[e]);
+        }
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), rs, (int)off[u], 0,
                                                kPolicyDeviceScope);
     }
