@@ -924,8 +924,9 @@ hipError_t launch_mma(const uint16_t *x, const uint8_t *w, uint16_t *y, size_t r
     constexpr size_t kRowsPerBlock = 16 * (kBlock / kWave);
     const dim3 grid((unsigned)((out + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)((rows + 15) / 16));
     // Q8_0 from 7 rows, rows at one phase to the 128-byte lines (in a
-    // multiple of 2048): each line loaded once (1.002 x the packed bytes
-    // instead of 1.134 x). [28672, 8192] over three boxes: 7, 8 and 16 rows
+    // multiple of 2048): each line of the weights loaded once (16 rows:
+    // 1.008 x the packed bytes with x read once per XCD, against 1.134 x at
+    // 4 rows without). [28672, 8192] over three boxes: 7, 8 and 16 rows
     // 1-3% faster that way, 3-6 rows 0.4-5% slower (the carry move and the
     // masked extra load pass sit on each step's critical path), so fewer
     // rows keep the per-chunk loads. Q4_0's 4-wave launches ran 12-14%
