@@ -1088,9 +1088,9 @@ def main():
                      "traffic": measured_traffic("cfg5_global_sum_max_f32"),
                      "algorithmic_bytes": global_bytes},
         "kernels": kernels,
-        "config_note": "the headline is configs[4]'s step (chain + global reduction) from the "
-                       "second round on; round 1 quoted configs[1] (f16 SiLU/GELU/SwiGLU), which "
-                       "`configs1` keeps reporting",
+        "config_note": "the headline is configs[4]'s step (chain + global reduction); the "
+                       "earlier headline, configs[1] (f16 SiLU/GELU/SwiGLU), is still reported "
+                       "under `configs1` for comparison",
     }
     if not args.no_suite:
         line["suite"] = suite(sdk, hip, stream)
@@ -1117,7 +1117,7 @@ def main():
         us = sum(suite_res[n]["avg_us"] for n in cfg1_names)
         line["configs1"] = {
             "workload": "BASELINE configs[1]: SiLU and tanh-GELU on [8192,8192] f16, SwiGLU on "
-                        "[4096,16384] f16 (the round-1 headline)",
+                        "[4096,16384] f16 (the earlier headline)",
             "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
             "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / PEAK_GBPS, 1),
             "kernels_us": {n: suite_res[n]["avg_us"] for n in cfg1_names}, "bytes": nbytes}
