@@ -350,7 +350,8 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     const float neg_inf = -__builtin_inff();
     R r;
     float m = neg_inf;
-    int pos_inf = 0;
+    // keys are < width < 2^32: the per-key test in 32 bits
+    const uint32_t limit32 = (uint32_t)min(limit, (uint64_t)0xffffffffu);
     // Vectors entirely past the causal limit re-read the row's first vector
     // (already requested by lane 0, so no HBM traffic) instead of branching.
     Vec16<S> raw[NV];
@@ -362,25 +363,32 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const uint64_t first = (uint64_t)(slot.t + j * R::T) * E;
+        const uint32_t first = (slot.t + j * R::T) * (uint32_t)E;
         const bool row_ok = slot.t + j * R::T < vpr;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             float s = Elem<S>::load(raw[j].v[e]);
-            s = row_ok && first + e <= limit ? s : neg_inf;
+            s = row_ok && first + e <= limit32 ? s : neg_inf;
             r.v[j][e] = s;
             m = fmaxf(m, s);
-            pos_inf += s == __builtin_inff();
         }
     }
     m = group_max<WPR>(m, lds);
-    pos_inf = group_sum_i32<WPR>(pos_inf, lds);
     if (m == neg_inf) {
 #pragma unroll
         for (int j = 0; j < NV; ++j)
 #pragma unroll
             for (int e = 0; e < E; ++e) r.v[j][e] = 0.0f;
-    } else if (pos_inf > 0) {
+    } else if (m == __builtin_inff()) {
+        // some visible key is +inf (fmaxf passes over NaN, so exactly then):
+        // the +inf keys share the row equally; counted only on this path
+        // (row-uniform: with several waves per row the block is the row)
+        int pos_inf = 0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < E; ++e) pos_inf += r.v[j][e] == __builtin_inff();
+        pos_inf = group_sum_i32<WPR>(pos_inf, lds);
         const float share = 1.0f / (float)pos_inf;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
