@@ -329,10 +329,14 @@ __device__ inline float softmax_exp(float x) {
 
 // Causal masking: key k of query row q is kept when k <= q + offset. A
 // vector whose first key is past the limit is never loaded.
+// Rows < 2^32 on this path, so the row's position in its query range is a
+// multiply-high division by q_len (q_mul, q_shift: FastDiv), kept in front of
+// the loads as a few scalar instructions.
 template <typename S, int NV, int WPR>
 __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x,
                                                          S *__restrict__ y, size_t rows,
                                                          uint32_t width, uint32_t q_len,
+                                                         uint32_t q_mul, uint32_t q_shift,
                                                          uint32_t causal_offset) {
     __shared__ float lds[kBlock / kWave];
     using R = RowRegs<S, NV, WPR>;
@@ -344,21 +348,25 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     const size_t row = live ? slot.row : rows - 1;
     const uint32_t vpr = width / E;
     const size_t base = row * width;
-    // keys 0..limit are visible
-    const uint64_t limit = q_len ? (uint64_t)(row % q_len) + causal_offset
-                                 : (uint64_t)width;
+    // keys 0..limit are visible (keys are < width < 2^32, so a limit past
+    // 2^32 - 1 is held at that)
+    uint32_t limit = width;
+    if (q_len) {
+        const uint32_t row32 = (uint32_t)row;
+        const uint64_t l = (uint64_t)(row32 - fast_div(row32, FastDiv{q_len, q_mul, q_shift}) * q_len) +
+                           causal_offset;
+        limit = (uint32_t)min(l, (uint64_t)0xffffffffu);
+    }
     const float neg_inf = -__builtin_inff();
     R r;
     float m = neg_inf;
-    // keys are < width < 2^32: the per-key test in 32 bits
-    const uint32_t limit32 = (uint32_t)min(limit, (uint64_t)0xffffffffu);
     // Vectors entirely past the causal limit re-read the row's first vector
     // (already requested by lane 0, so no HBM traffic) instead of branching.
     Vec16<S> raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const uint32_t vi = slot.t + j * R::T;
-        const bool use = vi < vpr && (uint64_t)vi * E <= limit;
+        const bool use = vi < vpr && vi * (uint32_t)E <= limit;
         raw[j] = load16_stream(x + base + (size_t)(use ? vi : 0u) * E);
     }
 #pragma unroll
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             float s = Elem<S>::load(raw[j].v[e]);
-            s = row_ok && first + e <= limit32 ? s : neg_inf;
+            s = row_ok && first + e <= limit ? s : neg_inf;
             r.v[j][e] = s;
             m = fmaxf(m, s);
         }
@@ -678,10 +686,13 @@ hipError_t launch_softmax(const S *x, S *y, size_t rows, size_t width, size_t q_
     const size_t offset = q_len && width > q_len ? width - q_len : 0;
     RowShape shape;
     const bool aligned = aligned16(x) && aligned16(y);
-    if (q_len <= 0xffffffffu && pick_row_shape(width, sizeof(S), aligned, &shape)) {
+    if (q_len <= 0xffffffffu && rows <= 0xffffffffu &&
+        pick_row_shape(width, sizeof(S), aligned, &shape)) {
+        const FastDiv qd = make_fast_div(q_len ? (uint32_t)q_len : 1u);
 #define ICSDK_SM(NV, WPR)                                                                  \
     hipLaunchKernelGGL((softmax_kernel<S, NV, WPR>), row_grid(rows, WPR), dim3(kBlock), 0, \
-                       s, x, y, rows, (uint32_t)width, (uint32_t)q_len, (uint32_t)offset)
+                       s, x, y, rows, (uint32_t)width, (uint32_t)q_len, qd.multiplier,      \
+                       qd.shift, (uint32_t)offset)
         ICSDK_ROW_DISPATCH(shape, ICSDK_SM);
 #undef ICSDK_SM
     } else {
