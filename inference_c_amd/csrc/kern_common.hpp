@@ -186,12 +186,30 @@ __device__ inline float wave_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Double-precision sum over the wave (cross-lane moves through ds_swizzle /
-// ds_bpermute via __shfl_xor; used only once per wave at the end of a grid
-// reduction).
+// Double-precision sum over the wave, the same DPP steps as wave_sum with
+// each double moved as its two 32-bit halves (a lane outside the row mask
+// receives 0.0: both halves 0).
+template <int kCtrl, int kRowMask = 0xf>
+__device__ inline double dpp_f64(double v) {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)bits, kCtrl,
+                                                              kRowMask, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(bits >> 32), kCtrl,
+                                                              kRowMask, 0xf, false);
+    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+
 __device__ inline double wave_sum_f64(double v) {
-    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
-    return v;
+    v += dpp_f64<kQuadSwap1>(v);
+    v += dpp_f64<kQuadSwap2>(v);
+    v += dpp_f64<kRowHalfMirror>(v);
+    v += dpp_f64<kRowMirror>(v);
+    v += dpp_f64<kRowBcast15, 0xa>(v);
+    v += dpp_f64<kRowBcast31, 0xc>(v);
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bits, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(bits >> 32), 63);
+    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
 }
 
 __device__ inline bool wave_any(bool flag) {
