@@ -329,9 +329,9 @@ __device__ inline float softmax_exp(float x) {
 
 // Causal masking: key k of query row q is kept when k <= q + offset. A
 // vector whose first key is past the limit is never loaded.
-// Rows < 2^32 on this path, so the row's position in its query range is a
-// multiply-high division by q_len (q_mul, q_shift: FastDiv), kept in front of
-// the loads as a few scalar instructions.
+// The row's position in its query range is a multiply-high division by
+// q_len (q_mul, q_shift: FastDiv) for rows below 2^32, kept in front of the
+// loads as a few scalar instructions.
 template <typename S, int NV, int WPR>
 __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x,
                                                          S *__restrict__ y, size_t rows,
@@ -353,9 +353,10 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(const S *__restrict__ x
     uint32_t limit = width;
     if (q_len) {
         const uint32_t row32 = (uint32_t)row;
-        const uint64_t l = (uint64_t)(row32 - fast_div(row32, FastDiv{q_len, q_mul, q_shift}) * q_len) +
-                           causal_offset;
-        limit = (uint32_t)min(l, (uint64_t)0xffffffffu);
+        // row-uniform: rows past 2^32 (never at real shapes) take the modulo
+        const uint32_t pos = row >> 32 ? (uint32_t)(row % q_len)
+                                       : row32 - fast_div(row32, FastDiv{q_len, q_mul, q_shift}) * q_len;
+        limit = (uint32_t)min((uint64_t)pos + causal_offset, (uint64_t)0xffffffffu);
     }
     const float neg_inf = -__builtin_inff();
     R r;
@@ -636,6 +637,8 @@ hipError_t launch_rms(const S *x, const S *residual, S *sum_out, const S *w, S *
         ICSDK_ROW_DISPATCH(shape, ICSDK_RMS);
 #undef ICSDK_RMS
     } else {
+        // one block per row: the grid's x dimension holds at most 2^32 - 1
+        if (rows > 0xffffffffu) return hipErrorInvalidValue;
         hipLaunchKernelGGL((rms_norm_stream_kernel<S, kResidual>), dim3((unsigned)rows),
                            dim3(kBlock), 0, s, x, residual, sum_out, w, y, rows, width, eps);
     }
@@ -673,6 +676,8 @@ hipError_t launch_layer(const S *x, const S *scale, const S *bias, S *y, size_t 
 #undef ICSDK_LN_AFF
 #undef ICSDK_LN_GO
     } else {
+        // one block per row: the grid's x dimension holds at most 2^32 - 1
+        if (rows > 0xffffffffu) return hipErrorInvalidValue;
         hipLaunchKernelGGL((layer_norm_stream_kernel<S>), dim3((unsigned)rows), dim3(kBlock),
                            0, s, x, scale, bias, y, rows, width, eps);
     }
@@ -686,8 +691,7 @@ hipError_t launch_softmax(const S *x, S *y, size_t rows, size_t width, size_t q_
     const size_t offset = q_len && width > q_len ? width - q_len : 0;
     RowShape shape;
     const bool aligned = aligned16(x) && aligned16(y);
-    if (q_len <= 0xffffffffu && rows <= 0xffffffffu &&
-        pick_row_shape(width, sizeof(S), aligned, &shape)) {
+    if (q_len <= 0xffffffffu && pick_row_shape(width, sizeof(S), aligned, &shape)) {
         const FastDiv qd = make_fast_div(q_len ? (uint32_t)q_len : 1u);
 #define ICSDK_SM(NV, WPR)                                                                  \
     hipLaunchKernelGGL((softmax_kernel<S, NV, WPR>), row_grid(rows, WPR), dim3(kBlock), 0, \
@@ -696,6 +700,8 @@ hipError_t launch_softmax(const S *x, S *y, size_t rows, size_t width, size_t q_
         ICSDK_ROW_DISPATCH(shape, ICSDK_SM);
 #undef ICSDK_SM
     } else {
+        // one block per row: the grid's x dimension holds at most 2^32 - 1
+        if (rows > 0xffffffffu) return hipErrorInvalidValue;
         hipLaunchKernelGGL((softmax_stream_kernel<S>), dim3((unsigned)rows), dim3(kBlock), 0,
                            s, x, y, rows, width, q_len, offset);
     }
@@ -714,6 +720,8 @@ hipError_t launch_row_reduce(const S *x, float *y, size_t rows, size_t width,
         ICSDK_ROW_DISPATCH(shape, ICSDK_RR);
 #undef ICSDK_RR
     } else {
+        // one block per row: the grid's x dimension holds at most 2^32 - 1
+        if (rows > 0xffffffffu) return hipErrorInvalidValue;
         hipLaunchKernelGGL((row_reduce_stream_kernel<S, kMax>), dim3((unsigned)rows),
                            dim3(kBlock), 0, s, x, y, rows, width);
     }
