@@ -497,6 +497,13 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
     measure("cfg4_permuted_broadcast_f16", cfg4,
             lambda s: sdk.call("tensor_view_add_mul_f16", s[0], view, s[1], s[2], s[3]),
             134_254_592, 33_554_432)
+    # a true transpose (the contiguous dim moves): [4096, 4096] f16, no operands
+    tview = TensorView.make((4096, 4096), (1, 4096), 0)
+    def transpose_set():
+        return (filled("f16", (4096, 4096), "normal", 4, 3, 0.0, 1.0), T("f16", (4096, 4096)))
+    measure("transpose_f16_4096", transpose_set,
+            lambda s: sdk.call("tensor_view_add_mul_f16", s[0], tview, None, None, s[1]),
+            67_108_864, 16_777_216)
     # cfg5: decoder chain (fused residual+RMSNorm, RoPE q+k, SwiGLU) timed as one chain
     tok, hid, inter = 4096, 2048, 8192
     def cfg5():

@@ -367,6 +367,68 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
     }
 }
 
+// Transposes of 2-byte elements without operands, in whole 16-byte vectors
+// (the tile's dims and every row start a multiple of 8 elements and 16-byte
+// aligned; the launcher checks): a tile's 64 x rows (64 elements along p,
+// contiguous in x) are read as 8 vectors each into LDS rows [l], vector c of
+// row l at slot c ^ (l / 8); each output row (64 elements along the last
+// dim, contiguous in y) is gathered from one LDS column, 8 reads per vector,
+// and written as 8 vectors. With the slot swizzle the 64 lanes of a gather
+// read 32 distinct banks (lanes 2m and 2m + 1 share a dword). The scalar
+// kernel below moves one element per lane per access.
+template <typename S>
+__global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(const S *__restrict__ x,
+                                                               S *__restrict__ y, TilePlan plan) {
+    static_assert(sizeof(S) == 2, "8 elements per 16-byte vector");
+    __shared__ u32x4 tile[kTile][kTile / 8];
+    const int last = plan.rank - 1;
+    const uint64_t block = blockIdx.x;
+    const uint32_t tl = (uint32_t)(block % plan.tiles_l);
+    const uint32_t tp = (uint32_t)((block / plan.tiles_l) % plan.tiles_p);
+    uint64_t batch = block / ((uint64_t)plan.tiles_l * plan.tiles_p);
+    int64_t xb = (int64_t)plan.x_offset;
+    uint64_t yb = 0;
+    for (int d = last - 1; d >= 0; --d) {
+        if (d == plan.p) continue;
+        const uint64_t idx = batch % plan.shape[d];
+        batch /= plan.shape[d];
+        xb += (int64_t)idx * plan.x_stride[d];
+        yb += idx * plan.y_stride[d];
+    }
+    const uint64_t p0 = (uint64_t)tp * kTile, l0 = (uint64_t)tl * kTile;
+    const uint64_t np = plan.shape[plan.p], nl = plan.shape[last];
+    const uint32_t c = threadIdx.x % 8;
+#pragma unroll
+    for (uint32_t pass = 0; pass < 2; ++pass) {
+        const uint32_t l = threadIdx.x / 8 + 32 * pass;
+        const uint64_t li = l0 + l, pi = p0 + 8 * c;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (li < nl && pi < np)
+            v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+                x + xb + (int64_t)li * plan.x_stride[last] + (int64_t)pi));
+        tile[l][c ^ (l / 8)] = v;
+    }
+    __syncthreads();
+    const uint64_t ys = plan.y_stride[plan.p];
+#pragma unroll
+    for (uint32_t pass = 0; pass < 2; ++pass) {
+        const uint32_t pr = threadIdx.x / 8 + 32 * pass;
+        const uint64_t pi = p0 + pr, li = l0 + 8 * c;
+        if (pi < np && li < nl) {
+            // element (l = 8c + k, p = pr): row l, slot (pr / 8) ^ c, half pr % 8
+            uint32_t h[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const uint16_t *row = reinterpret_cast<const uint16_t *>(&tile[8 * c + k][0]);
+                h[k] = row[(((pr / 8) ^ c) * 8) + pr % 8];
+            }
+            const u32x4 o = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
+                                  h[6] | h[7] << 16};
+            *reinterpret_cast<u32x4 *>(y + yb + pi * ys + li) = o;
+        }
+    }
+}
+
 inline bool aligned16(const void *p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
 // Gather-path plan for a coalesced view, or false when the view does not fit
@@ -527,6 +589,20 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
         plan.tiles_l = (uint32_t)((c.shape[last] + kTile - 1) / kTile);
         const uint64_t blocks = plan.batches * plan.tiles_p * plan.tiles_l;
         if (blocks < (uint64_t{1} << 31)) {
+            if constexpr (sizeof(S) == 2) {
+                // whole 16-byte vectors: p and last a multiple of 8 elements,
+                // every x row and batch offset too, both tensors 16-byte aligned
+                bool vec = addend == nullptr && mult == nullptr && c.shape[p] % 8 == 0 &&
+                           c.shape[last] % 8 == 0 && v.offset % 8 == 0 &&
+                           ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0;
+                for (int d = 0; d <= last; ++d)
+                    if (d != p && c.x_stride[d] % 8 != 0) vec = false;
+                if (vec) {
+                    hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)blocks),
+                                       dim3(kBlock), 0, s, x, y, plan);
+                    return hipGetLastError();
+                }
+            }
             hipLaunchKernelGGL((view_tile_kernel<S>), dim3((unsigned)blocks), dim3(kBlock), 0,
                                s, x, addend, mult, y, plan);
             return hipGetLastError();

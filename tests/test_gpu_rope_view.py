@@ -123,7 +123,7 @@ def test_config4_permuted_broadcast(sdk, orc, device):
 
 
 @pytest.mark.parametrize("case", ["vector_tile", "vector_tile_ragged", "vector_rows", "tile",
-                                  "scalar", "broadcast_x", "offset", "rank1", "coalesce_contig",
+                                  "tile_vec", "tile_vec_offset", "scalar", "broadcast_x", "offset", "rank1", "coalesce_contig",
                                   "rank6", "unit_dims", "one_vector_runs", "addend_inner_bcast",
                                   "short_rank4", "short_rank3_offset", "short_rank2",
                                   "copy_whole", "copy_ragged", "copy_unaligned"])
@@ -152,6 +152,16 @@ def test_view_paths(sdk, orc, case, dtype):
         shape, strides, off = (2, 3, 130, 70), (3 * 70 * 130, 70 * 130, 1, 130), 0
         A = orc.uniform((1, 3, 130, 1), 53, 1, -1, 1, dt)
         M = orc.uniform((2, 1, 1, 70), 53, 2, -1, 1, dt)
+    elif case == "tile_vec":   # transpose in whole 16-byte vectors (f16 without
+        # operands: the vector tile kernel), partial 64 x 64 tiles, two batch dims
+        x = orc.normal((2, 3, 72, 136), 71, 0, 0.0, 1.0, dt)
+        shape, strides, off = (2, 3, 136, 72), (3 * 72 * 136, 72 * 136, 1, 136), 0
+        A = orc.uniform((1, 3, 136, 1), 71, 1, -1, 1, dt)
+        M = orc.uniform((2, 1, 1, 72), 71, 2, -1, 1, dt)
+    elif case == "tile_vec_offset":  # a 16-column slice at an offset, transposed
+        x = orc.normal((1000, 24), 72, 0, 0.0, 1.0, dt)
+        shape, strides, off = (16, 1000), (1, 24), 8
+        A, M = orc.uniform((16, 1), 72, 1, -1, 1, dt), None
     elif case == "scalar":     # odd strides
         x = orc.normal((1000,), 54, 0, 0.0, 1.0, dt)
         shape, strides, off = (7, 9), (101, 3), 5
