@@ -376,44 +376,52 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
 // and written as 8 vectors. With the slot swizzle the 64 lanes of a gather
 // read 32 distinct banks (lanes 2m and 2m + 1 share a dword). The scalar
 // kernel below moves one element per lane per access.
+//
+// Everything a wave needs before its first load arrives as a plain scalar
+// argument (preloaded in SGPRs; the tile grid split by multiply-high
+// divisions); the plan is read only by blocks past the first batch.
 template <typename S>
-__global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(const S *__restrict__ x,
-                                                               S *__restrict__ y, TilePlan plan) {
+__global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
+    const S *__restrict__ x, S *__restrict__ y, uint32_t tiles_l, uint32_t tl_mul,
+    uint32_t tl_shift, uint32_t tiles_p, uint32_t tp_mul, uint32_t tp_shift, uint32_t np,
+    uint32_t nl, uint32_t xs_last, uint32_t x_offset, uint32_t ys, TilePlan plan) {
     static_assert(sizeof(S) == 2, "8 elements per 16-byte vector");
     __shared__ u32x4 tile[kTile][kTile / 8];
-    const int last = plan.rank - 1;
-    const uint64_t block = blockIdx.x;
-    const uint32_t tl = (uint32_t)(block % plan.tiles_l);
-    const uint32_t tp = (uint32_t)((block / plan.tiles_l) % plan.tiles_p);
-    uint64_t batch = block / ((uint64_t)plan.tiles_l * plan.tiles_p);
-    int64_t xb = (int64_t)plan.x_offset;
+    const uint32_t block = blockIdx.x;
+    const uint32_t rest = fast_div(block, FastDiv{tiles_l, tl_mul, tl_shift});
+    const uint32_t tl = block - rest * tiles_l;
+    uint32_t batch = fast_div(rest, FastDiv{tiles_p, tp_mul, tp_shift});
+    const uint32_t tp = rest - batch * tiles_p;
+    int64_t xb = (int64_t)x_offset;
     uint64_t yb = 0;
-    for (int d = last - 1; d >= 0; --d) {
-        if (d == plan.p) continue;
-        const uint64_t idx = batch % plan.shape[d];
-        batch /= plan.shape[d];
-        xb += (int64_t)idx * plan.x_stride[d];
-        yb += idx * plan.y_stride[d];
+    if (batch != 0) {   // block-uniform; batch 0 has every batch index 0
+        const int last = plan.rank - 1;
+        uint64_t b = batch;
+        for (int d = last - 1; d >= 0; --d) {
+            if (d == plan.p) continue;
+            const uint64_t idx = b % plan.shape[d];
+            b /= plan.shape[d];
+            xb += (int64_t)idx * plan.x_stride[d];
+            yb += idx * plan.y_stride[d];
+        }
     }
-    const uint64_t p0 = (uint64_t)tp * kTile, l0 = (uint64_t)tl * kTile;
-    const uint64_t np = plan.shape[plan.p], nl = plan.shape[last];
+    const uint32_t p0 = tp * kTile, l0 = tl * kTile;
     const uint32_t c = threadIdx.x % 8;
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t l = threadIdx.x / 8 + 32 * pass;
-        const uint64_t li = l0 + l, pi = p0 + 8 * c;
+        const uint32_t li = l0 + l, pi = p0 + 8 * c;
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (li < nl && pi < np)
             v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-                x + xb + (int64_t)li * plan.x_stride[last] + (int64_t)pi));
+                x + xb + (int64_t)li * xs_last + pi));
         tile[l][c ^ (l / 8)] = v;
     }
     __syncthreads();
-    const uint64_t ys = plan.y_stride[plan.p];
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t pr = threadIdx.x / 8 + 32 * pass;
-        const uint64_t pi = p0 + pr, li = l0 + 8 * c;
+        const uint32_t pi = p0 + pr, li = l0 + 8 * c;
         if (pi < np && li < nl) {
             // element (l = 8c + k, p = pr): row l, slot (pr / 8) ^ c, half pr % 8
             uint32_t h[8];
@@ -424,7 +432,7 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(const S *__restri
             }
             const u32x4 o = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
                                   h[6] | h[7] << 16};
-            *reinterpret_cast<u32x4 *>(y + yb + pi * ys + li) = o;
+            *reinterpret_cast<u32x4 *>(y + yb + (uint64_t)pi * ys + li) = o;
         }
     }
 }
@@ -592,14 +600,25 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
             if constexpr (sizeof(S) == 2) {
                 // whole 16-byte vectors: p and last a multiple of 8 elements,
                 // every x row and batch offset too, both tensors 16-byte aligned
+                // (the scalar arguments hold dims, the x row stride, the
+                // offset and the output row stride in 32 bits)
+                const uint64_t lim = 0xffffffffull;
                 bool vec = addend == nullptr && mult == nullptr && c.shape[p] % 8 == 0 &&
                            c.shape[last] % 8 == 0 && v.offset % 8 == 0 &&
-                           ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0;
+                           ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0 &&
+                           c.shape[p] + kTile <= lim && c.shape[last] + kTile <= lim &&
+                           c.x_stride[last] > 0 && (uint64_t)c.x_stride[last] <= lim &&
+                           v.offset <= lim && plan.y_stride[p] <= lim;
                 for (int d = 0; d <= last; ++d)
                     if (d != p && c.x_stride[d] % 8 != 0) vec = false;
                 if (vec) {
+                    const FastDiv dl = make_fast_div(plan.tiles_l), dp = make_fast_div(plan.tiles_p);
                     hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)blocks),
-                                       dim3(kBlock), 0, s, x, y, plan);
+                                       dim3(kBlock), 0, s, x, y, plan.tiles_l, dl.multiplier,
+                                       dl.shift, plan.tiles_p, dp.multiplier, dp.shift,
+                                       (uint32_t)c.shape[p], (uint32_t)c.shape[last],
+                                       (uint32_t)c.x_stride[last], (uint32_t)v.offset,
+                                       (uint32_t)plan.y_stride[p], plan);
                     return hipGetLastError();
                 }
             }
