@@ -374,7 +374,9 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
 // row l at slot c ^ (l / 8); each output row (64 elements along the last
 // dim, contiguous in y) is gathered from one LDS column, 8 reads per vector,
 // and written as 8 vectors. With the slot swizzle the 64 lanes of a gather
-// read 32 distinct banks (lanes 2m and 2m + 1 share a dword). The scalar
+// read 32 distinct banks (lanes 2m and 2m + 1 share a dword). A block takes
+// two tiles along the last dim, all four of a lane's loads issued first
+// ([4096, 4096]: 15.0 -> 13.1 us against one tile per block). The scalar
 // kernel below moves one element per lane per access.
 //
 // Everything a wave needs before its first load arrives as a plain scalar
@@ -386,7 +388,7 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
     uint32_t tl_shift, uint32_t tiles_p, uint32_t tp_mul, uint32_t tp_shift, uint32_t np,
     uint32_t nl, uint32_t xs_last, uint32_t x_offset, uint32_t ys, TilePlan plan) {
     static_assert(sizeof(S) == 2, "8 elements per 16-byte vector");
-    __shared__ u32x4 tile[kTile][kTile / 8];
+    __shared__ u32x4 tile[2][kTile][kTile / 8];
     const uint32_t block = blockIdx.x;
     const uint32_t rest = fast_div(block, FastDiv{tiles_l, tl_mul, tl_shift});
     const uint32_t tl = block - rest * tiles_l;
@@ -405,29 +407,33 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
             yb += idx * plan.y_stride[d];
         }
     }
-    const uint32_t p0 = tp * kTile, l0 = tl * kTile;
+    const uint32_t p0 = tp * kTile, l0 = tl * (2 * kTile);
     const uint32_t c = threadIdx.x % 8;
+#pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t l = threadIdx.x / 8 + 32 * pass;
-        const uint32_t li = l0 + l, pi = p0 + 8 * c;
+        const uint32_t li = l0 + kTile * tt + l, pi = p0 + 8 * c;
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (li < nl && pi < np)
             v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
                 x + xb + (int64_t)li * xs_last + pi));
-        tile[l][c ^ (l / 8)] = v;
+        tile[tt][l][c ^ (l / 8)] = v;
     }
     __syncthreads();
 #pragma unroll
+    for (uint32_t tt = 0; tt < 2; ++tt)
+#pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t pr = threadIdx.x / 8 + 32 * pass;
-        const uint32_t pi = p0 + pr, li = l0 + 8 * c;
+        const uint32_t pi = p0 + pr, li = l0 + kTile * tt + 8 * c;
         if (pi < np && li < nl) {
             // element (l = 8c + k, p = pr): row l, slot (pr / 8) ^ c, half pr % 8
             uint32_t h[8];
 #pragma unroll
             for (uint32_t k = 0; k < 8; ++k) {
-                const uint16_t *row = reinterpret_cast<const uint16_t *>(&tile[8 * c + k][0]);
+                const uint16_t *row = reinterpret_cast<const uint16_t *>(&tile[tt][8 * c + k][0]);
                 h[k] = row[(((pr / 8) ^ c) * 8) + pr % 8];
             }
             const u32x4 o = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
@@ -612,9 +618,11 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
                 for (int d = 0; d <= last; ++d)
                     if (d != p && c.x_stride[d] % 8 != 0) vec = false;
                 if (vec) {
-                    const FastDiv dl = make_fast_div(plan.tiles_l), dp = make_fast_div(plan.tiles_p);
-                    hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)blocks),
-                                       dim3(kBlock), 0, s, x, y, plan.tiles_l, dl.multiplier,
+                    const uint32_t pairs_l = (plan.tiles_l + 1) / 2;
+                    const uint64_t vblocks = plan.batches * plan.tiles_p * pairs_l;
+                    const FastDiv dl = make_fast_div(pairs_l), dp = make_fast_div(plan.tiles_p);
+                    hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)vblocks),
+                                       dim3(kBlock), 0, s, x, y, pairs_l, dl.multiplier,
                                        dl.shift, plan.tiles_p, dp.multiplier, dp.shift,
                                        (uint32_t)c.shape[p], (uint32_t)c.shape[last],
                                        (uint32_t)c.x_stride[last], (uint32_t)v.offset,
