@@ -375,20 +375,21 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
 // dim, contiguous in y) is gathered from one LDS column, 8 reads per vector,
 // and written as 8 vectors. With the slot swizzle the 64 lanes of a gather
 // read 32 distinct banks (lanes 2m and 2m + 1 share a dword). A block takes
-// two tiles along the last dim, all four of a lane's loads issued first
-// ([4096, 4096]: 15.0 -> 13.1 us against one tile per block). The scalar
-// kernel below moves one element per lane per access.
+// kVecTiles tiles along the last dim, all of a lane's loads issued first
+// ([4096, 4096]: one tile per block 15.0 us, two 13.1, four 12.7-12.8). The
+// scalar kernel below moves one element per lane per access.
 //
 // Everything a wave needs before its first load arrives as a plain scalar
 // argument (preloaded in SGPRs; the tile grid split by multiply-high
 // divisions); the plan is read only by blocks past the first batch.
+constexpr uint32_t kVecTiles = 4;   // 64 x 64 tiles per block along the last dim
 template <typename S>
 __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
     const S *__restrict__ x, S *__restrict__ y, uint32_t tiles_l, uint32_t tl_mul,
     uint32_t tl_shift, uint32_t tiles_p, uint32_t tp_mul, uint32_t tp_shift, uint32_t np,
     uint32_t nl, uint32_t xs_last, uint32_t x_offset, uint32_t ys, TilePlan plan) {
     static_assert(sizeof(S) == 2, "8 elements per 16-byte vector");
-    __shared__ u32x4 tile[2][kTile][kTile / 8];
+    __shared__ u32x4 tile[kVecTiles][kTile][kTile / 8];
     const uint32_t block = blockIdx.x;
     const uint32_t rest = fast_div(block, FastDiv{tiles_l, tl_mul, tl_shift});
     const uint32_t tl = block - rest * tiles_l;
@@ -407,10 +408,10 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
             yb += idx * plan.y_stride[d];
         }
     }
-    const uint32_t p0 = tp * kTile, l0 = tl * (2 * kTile);
+    const uint32_t p0 = tp * kTile, l0 = tl * (kVecTiles * kTile);
     const uint32_t c = threadIdx.x % 8;
 #pragma unroll
-    for (uint32_t tt = 0; tt < 2; ++tt)
+    for (uint32_t tt = 0; tt < kVecTiles; ++tt)
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t l = threadIdx.x / 8 + 32 * pass;
@@ -423,7 +424,7 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t tt = 0; tt < 2; ++tt)
+    for (uint32_t tt = 0; tt < kVecTiles; ++tt)
 #pragma unroll
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t pr = threadIdx.x / 8 + 32 * pass;
@@ -618,7 +619,7 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
                 for (int d = 0; d <= last; ++d)
                     if (d != p && c.x_stride[d] % 8 != 0) vec = false;
                 if (vec) {
-                    const uint32_t pairs_l = (plan.tiles_l + 1) / 2;
+                    const uint32_t pairs_l = (plan.tiles_l + kVecTiles - 1) / kVecTiles;
                     const uint64_t vblocks = plan.batches * plan.tiles_p * pairs_l;
                     const FastDiv dl = make_fast_div(pairs_l), dp = make_fast_div(plan.tiles_p);
                     hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)vblocks),
