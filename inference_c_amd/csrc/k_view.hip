@@ -28,6 +28,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace icsdk {
 namespace {
@@ -367,14 +368,15 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
     }
 }
 
-// Transposes of 2-byte elements without operands, in whole 16-byte vectors
-// (the tile's dims and every row start a multiple of 8 elements and 16-byte
-// aligned; the launcher checks): a tile's 64 x rows (64 elements along p,
-// contiguous in x) are read as 8 vectors each into LDS rows [l], vector c of
-// row l at slot c ^ (l / 8); each output row (64 elements along the last
-// dim, contiguous in y) is gathered from one LDS column, 8 reads per vector,
-// and written as 8 vectors. With the slot swizzle the 64 lanes of a gather
-// read 32 distinct banks (lanes 2m and 2m + 1 share a dword). A block takes
+// Transposes without operands in whole 16-byte vectors of E elements (8 for
+// f16, 4 for f32; the tile's dims and every row start a multiple of E
+// elements and 16-byte aligned; the launcher checks): a tile's 64 x rows (64
+// elements along p, contiguous in x) are read as 64 / E vectors each into LDS
+// rows [l], vector c of row l at slot c ^ (l / E); each output row (64
+// elements along the last dim, contiguous in y) is gathered from one LDS
+// column, E reads per vector, and written as 64 / E vectors. With the slot
+// swizzle the 64 lanes of a gather read distinct banks (f16: 32, lanes 2m
+// and 2m + 1 sharing a dword; f32: 64). A block takes
 // kVecTiles tiles along the last dim, all of a lane's loads issued first
 // ([4096, 4096]: one tile per block 15.0 us, two 13.1, four 12.7-12.8). The
 // scalar kernel below moves one element per lane per access.
@@ -382,14 +384,21 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
 // Everything a wave needs before its first load arrives as a plain scalar
 // argument (preloaded in SGPRs; the tile grid split by multiply-high
 // divisions); the plan is read only by blocks past the first batch.
-constexpr uint32_t kVecTiles = 4;   // 64 x 64 tiles per block along the last dim
+// 64 x 64 tiles per block along the last dim: 4 for 2-byte elements, 2 for
+// f32 (32 KB of LDS either way)
+template <typename S> constexpr uint32_t kVecTiles = sizeof(S) == 2 ? 4 : 2;
 template <typename S>
 __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
     const S *__restrict__ x, S *__restrict__ y, uint32_t tiles_l, uint32_t tl_mul,
     uint32_t tl_shift, uint32_t tiles_p, uint32_t tp_mul, uint32_t tp_shift, uint32_t np,
     uint32_t nl, uint32_t xs_last, uint32_t x_offset, uint32_t ys, TilePlan plan) {
-    static_assert(sizeof(S) == 2, "8 elements per 16-byte vector");
-    __shared__ u32x4 tile[kVecTiles][kTile][kTile / 8];
+    static_assert(sizeof(S) == 2 || sizeof(S) == 4, "2- or 4-byte elements");
+    constexpr uint32_t E = Vec16<S>::N;              // elements per 16-byte vector
+    constexpr uint32_t kSlots = kTile / E;           // vectors per 64-element row
+    constexpr uint32_t kRowsPerPass = kBlock / kSlots;
+    constexpr uint32_t kTiles = kVecTiles<S>;
+    using U = std::conditional_t<sizeof(S) == 2, uint16_t, uint32_t>;
+    __shared__ u32x4 tile[kTiles][kTile][kSlots];
     const uint32_t block = blockIdx.x;
     const uint32_t rest = fast_div(block, FastDiv{tiles_l, tl_mul, tl_shift});
     const uint32_t tl = block - rest * tiles_l;
@@ -408,37 +417,40 @@ __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
             yb += idx * plan.y_stride[d];
         }
     }
-    const uint32_t p0 = tp * kTile, l0 = tl * (kVecTiles * kTile);
-    const uint32_t c = threadIdx.x % 8;
+    const uint32_t p0 = tp * kTile, l0 = tl * (kTiles * kTile);
+    const uint32_t c = threadIdx.x % kSlots;
 #pragma unroll
-    for (uint32_t tt = 0; tt < kVecTiles; ++tt)
+    for (uint32_t tt = 0; tt < kTiles; ++tt)
 #pragma unroll
-    for (uint32_t pass = 0; pass < 2; ++pass) {
-        const uint32_t l = threadIdx.x / 8 + 32 * pass;
-        const uint32_t li = l0 + kTile * tt + l, pi = p0 + 8 * c;
+    for (uint32_t pass = 0; pass < kTile / kRowsPerPass; ++pass) {
+        const uint32_t l = threadIdx.x / kSlots + kRowsPerPass * pass;
+        const uint32_t li = l0 + kTile * tt + l, pi = p0 + E * c;
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (li < nl && pi < np)
             v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
                 x + xb + (int64_t)li * xs_last + pi));
-        tile[tt][l][c ^ (l / 8)] = v;
+        tile[tt][l][c ^ (l / E % kSlots)] = v;
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t tt = 0; tt < kVecTiles; ++tt)
+    for (uint32_t tt = 0; tt < kTiles; ++tt)
 #pragma unroll
-    for (uint32_t pass = 0; pass < 2; ++pass) {
-        const uint32_t pr = threadIdx.x / 8 + 32 * pass;
-        const uint32_t pi = p0 + pr, li = l0 + kTile * tt + 8 * c;
+    for (uint32_t pass = 0; pass < kTile / kRowsPerPass; ++pass) {
+        const uint32_t pr = threadIdx.x / kSlots + kRowsPerPass * pass;
+        const uint32_t pi = p0 + pr, li = l0 + kTile * tt + E * c;
         if (pi < np && li < nl) {
-            // element (l = 8c + k, p = pr): row l, slot (pr / 8) ^ c, half pr % 8
-            uint32_t h[8];
+            // element (l = E c + k, p = pr): row l, slot (pr / E) ^ c, element pr % E
+            uint32_t h[E];
 #pragma unroll
-            for (uint32_t k = 0; k < 8; ++k) {
-                const uint16_t *row = reinterpret_cast<const uint16_t *>(&tile[tt][8 * c + k][0]);
-                h[k] = row[(((pr / 8) ^ c) * 8) + pr % 8];
+            for (uint32_t k = 0; k < E; ++k) {
+                const U *row = reinterpret_cast<const U *>(&tile[tt][E * c + k][0]);
+                h[k] = row[(((pr / E) ^ c) * E) + pr % E];
             }
-            const u32x4 o = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
-                                  h[6] | h[7] << 16};
+            u32x4 o;
+            if constexpr (sizeof(S) == 2)
+                o = u32x4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
+            else
+                o = u32x4{h[0], h[1], h[2], h[3]};
             *reinterpret_cast<u32x4 *>(y + yb + (uint64_t)pi * ys + li) = o;
         }
     }
@@ -604,22 +616,23 @@ hipError_t launch_view(const S *x, const k::ViewArgs &v, const S *addend,
         plan.tiles_l = (uint32_t)((c.shape[last] + kTile - 1) / kTile);
         const uint64_t blocks = plan.batches * plan.tiles_p * plan.tiles_l;
         if (blocks < (uint64_t{1} << 31)) {
-            if constexpr (sizeof(S) == 2) {
-                // whole 16-byte vectors: p and last a multiple of 8 elements,
+            {
+                // whole 16-byte vectors: p and last a multiple of E elements,
                 // every x row and batch offset too, both tensors 16-byte aligned
                 // (the scalar arguments hold dims, the x row stride, the
                 // offset and the output row stride in 32 bits)
                 const uint64_t lim = 0xffffffffull;
-                bool vec = addend == nullptr && mult == nullptr && c.shape[p] % 8 == 0 &&
-                           c.shape[last] % 8 == 0 && v.offset % 8 == 0 &&
+                constexpr uint64_t E = Vec16<S>::N;
+                bool vec = addend == nullptr && mult == nullptr && c.shape[p] % E == 0 &&
+                           c.shape[last] % E == 0 && v.offset % E == 0 &&
                            ((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0 &&
                            c.shape[p] + kTile <= lim && c.shape[last] + kTile <= lim &&
                            c.x_stride[last] > 0 && (uint64_t)c.x_stride[last] <= lim &&
                            v.offset <= lim && plan.y_stride[p] <= lim;
                 for (int d = 0; d <= last; ++d)
-                    if (d != p && c.x_stride[d] % 8 != 0) vec = false;
+                    if (d != p && c.x_stride[d] % (int64_t)E != 0) vec = false;
                 if (vec) {
-                    const uint32_t pairs_l = (plan.tiles_l + kVecTiles - 1) / kVecTiles;
+                    const uint32_t pairs_l = (plan.tiles_l + kVecTiles<S> - 1) / kVecTiles<S>;
                     const uint64_t vblocks = plan.batches * plan.tiles_p * pairs_l;
                     const FastDiv dl = make_fast_div(pairs_l), dp = make_fast_div(plan.tiles_p);
                     hipLaunchKernelGGL((view_tile_vec_kernel<S>), dim3((unsigned)vblocks),
