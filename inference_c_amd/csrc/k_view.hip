@@ -384,9 +384,9 @@ __global__ __launch_bounds__(kBlock) void view_tile_kernel(const S *__restrict__
 // Everything a wave needs before its first load arrives as a plain scalar
 // argument (preloaded in SGPRs; the tile grid split by multiply-high
 // divisions); the plan is read only by blocks past the first batch.
-// 64 x 64 tiles per block along the last dim: 4 for 2-byte elements, 2 for
-// f32 (32 KB of LDS either way)
-template <typename S> constexpr uint32_t kVecTiles = sizeof(S) == 2 ? 4 : 2;
+// 64 x 64 tiles per block along the last dim: 4 for 2-byte elements (32 KB
+// of LDS), 1 for f32 (16 KB; f32 [4096, 4096]: 29.7 us with 2, 27.7 with 1)
+template <typename S> constexpr uint32_t kVecTiles = sizeof(S) == 2 ? 4 : 1;
 template <typename S>
 __global__ __launch_bounds__(kBlock) void view_tile_vec_kernel(
     const S *__restrict__ x, S *__restrict__ y, uint32_t tiles_l, uint32_t tl_mul,
