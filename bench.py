@@ -504,6 +504,11 @@ def suite(sdk, hip, stream, reps=20, rounds=5, only=None):
     measure("transpose_f16_4096", transpose_set,
             lambda s: sdk.call("tensor_view_add_mul_f16", s[0], tview, None, None, s[1]),
             67_108_864, 16_777_216)
+    def transpose_set_f32():
+        return (filled("f32", (4096, 4096), "normal", 4, 4, 0.0, 1.0), T("f32", (4096, 4096)))
+    measure("transpose_f32_4096", transpose_set_f32,
+            lambda s: sdk.call("tensor_view_add_mul_f32", s[0], tview, None, None, s[1]),
+            134_217_728, 16_777_216)
     # cfg5: decoder chain (fused residual+RMSNorm, RoPE q+k, SwiGLU) timed as one chain
     tok, hid, inter = 4096, 2048, 8192
     def cfg5():
